@@ -1,0 +1,201 @@
+// Shared device helpers for the gfx950 compressed-KV kernels.
+//
+// Everything here is compiled with -ffp-contract=off: each fp32 add/mul rounds
+// once, in program order, so the CPU oracle can reproduce the codec and the
+// tile scores bit for bit.  Explicit fmaf() is used only where a result is a
+// tolerance (attention), never on a bit-exact path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kvr_capi.h"
+
+namespace kvr {
+
+constexpr int D = 128;                // head_dim
+constexpr float C_HAD = 0x1.6a09e6p-4f;  // fp32(2^-3.5) = 0x3db504f3
+constexpr float EPS = 1e-8f;
+constexpr float FP16_MAX = 65504.0f;
+constexpr float LOG2E = 1.4426950408889634f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ conversions
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t raw16) { return __uint_as_float(raw16 << 16); }
+
+__device__ __forceinline__ float f16_to_f32(uint32_t raw16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)raw16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bit pattern (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Load element i of a bf16 / fp16 / fp32 array as fp32 (exact).
+template <int DT>
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
+  if constexpr (DT == KVR_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+  else if constexpr (DT == KVR_FP16) return f16_to_f32(((const uint16_t*)p)[i]);
+  else return ((const float*)p)[i];
+}
+
+// Correctly rounded fp32 square root: the f64 root of an f32 is correctly
+// rounded to 53 bits, and 53 >= 2*24+2, so rounding it to f32 is correct.
+__device__ __forceinline__ float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
+
+// ------------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int m) {
+  return (uint32_t)__shfl_xor((int)v, m, 64);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = v + shfl_xor_f(v, m);
+  return v;
+}
+
+// One FWHT butterfly stage across lanes for a value held one-per-lane:
+// lanes with (lane & m) == 0 hold the lower element of each pair.
+// Lower: a + b; upper: a - b (a = lower value, b = upper value) -- the same
+// single fp32 add/sub the oracle performs.
+__device__ __forceinline__ float fwht_xlane(float v, int lane, int m) {
+  float p = shfl_xor_f(v, m);
+  return (lane & m) ? (p - v) : (v + p);
+}
+
+// Full orthonormal Hadamard-128 (spec order h = 1..64, then * C_HAD) of a
+// vector held as channels (2*lane, 2*lane+1) in (v0, v1).  Bit-exact.
+__device__ __forceinline__ void hadamard_pair(float& v0, float& v1, int lane) {
+  float a = v0 + v1, b = v0 - v1;  // h = 1
+  v0 = a;
+  v1 = b;
+#pragma unroll
+  for (int m = 1; m <= 32; m <<= 1) {  // h = 2m: partner lane = lane ^ m
+    v0 = fwht_xlane(v0, lane, m);
+    v1 = fwht_xlane(v1, lane, m);
+  }
+  v0 = v0 * C_HAD;
+  v1 = v1 * C_HAD;
+}
+
+// In-register unnormalised FWHT of 128 values (spec order), bit-exact.
+__device__ __forceinline__ void fwht128_regs(float* x) {
+#pragma unroll
+  for (int h = 1; h < 128; h <<= 1) {
+#pragma unroll
+    for (int j = 0; j < 128; ++j) {
+      if ((j & h) == 0) {
+        float a = x[j], b = x[j + h];
+        x[j] = a + b;
+        x[j + h] = a - b;
+      }
+    }
+  }
+}
+
+// Orthonormal DCT-II matrix C[k][n] = a_k cos(pi (2n+1) k / 256), fp32, row k =
+// frequency.  Built at compile time: only the 512 angles pi*r/256 occur, each
+// evaluated in double by a Taylor series on [0, pi/2] (error < 1e-16), then
+// scaled by a_0 = sqrt(1/128) or a_k = 1/8 and rounded once to fp32.
+struct DctTable {
+  float v[D * D];
+};
+
+constexpr double cos_pi_r256(int r) {  // cos(pi * r / 256), r in [0, 512)
+  double sign = 1.0;
+  if (r > 256) r = 512 - r;
+  if (r > 128) {
+    r = 256 - r;
+    sign = -1.0;
+  }
+  const double x = 3.14159265358979323846 * (double)r / 256.0;
+  double term = 1.0, sum = 1.0;
+  for (int i = 1; i < 20; ++i) {
+    term *= -x * x / (double)((2 * i - 1) * (2 * i));
+    sum += term;
+  }
+  return sign * sum;
+}
+
+constexpr DctTable make_dct_table() {
+  DctTable t{};
+  double c[512] = {};
+  for (int r = 0; r < 512; ++r) c[r] = cos_pi_r256(r);
+  for (int k = 0; k < D; ++k) {
+    const double a = (k == 0) ? 0.088388347648318440550 : 0.125;
+    for (int n = 0; n < D; ++n) t.v[k * D + n] = (float)(a * c[((2 * n + 1) * k) % 512]);
+  }
+  return t;
+}
+
+static __constant__ DctTable g_dct_tab = make_dct_table();
+#define g_dct (g_dct_tab.v)
+
+// y = C x for a vector held as channels (2*lane, 2*lane+1); x is staged in
+// the caller's LDS buffer xs[128].  Tolerance path (fmaf allowed).
+__device__ __forceinline__ void dct_pair(float& v0, float& v1, int lane, float* xs) {
+  xs[2 * lane] = v0;
+  xs[2 * lane + 1] = v1;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  float a0 = 0.f, a1 = 0.f;
+  const float* r0 = g_dct + (2 * lane) * D;
+  const float* r1 = r0 + D;
+#pragma unroll 8
+  for (int n = 0; n < D; ++n) {
+    float x = xs[n];
+    a0 = fmaf(r0[n], x, a0);
+    a1 = fmaf(r1[n], x, a1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  v0 = a0;
+  v1 = a1;
+}
+
+// x = C^T y for a vector held as channels (2*lane, 2*lane+1).
+__device__ __forceinline__ void idct_pair(float& v0, float& v1, int lane, float* xs) {
+  xs[2 * lane] = v0;
+  xs[2 * lane + 1] = v1;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll 8
+  for (int k = 0; k < D; ++k) {
+    float y = xs[k];
+    a0 = fmaf(g_dct[k * D + 2 * lane], y, a0);
+    a1 = fmaf(g_dct[k * D + 2 * lane + 1], y, a1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  v0 = a0;
+  v1 = a1;
+}
+
+// Orderable key of an fp32 score: larger float -> larger key; NaN -> -inf.
+__device__ __forceinline__ uint32_t score_key(float f) {
+  if (f != f) f = -__builtin_inff();
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+}  // namespace kvr

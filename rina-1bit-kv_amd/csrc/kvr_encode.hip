@@ -1,0 +1,180 @@
+// Subsystem 1: fused tile encoder (rotation -> per-tile fp16 scale ->
+// sigma-delta 1-bit along tokens -> packed channel words).
+//
+// One 64-lane workgroup per (segment, tile).  Phase A: lane = token, the
+// token's 128 channels are loaded into registers and rotated (Hadamard as an
+// in-register FWHT in the codec's fixed stage order; DCT-II as a matrix-vector
+// product with the matrix in constant memory), then stored transposed into
+// LDS as [channel][token].  Phase B: lane = channel pair (lane, lane+64); the
+// per-channel |y| sums run sequentially over tokens and feed the fixed
+// stride-halving tree, then each lane runs the sigma-delta recurrence for its
+// two channels and writes their uint64 words (coalesced, 512 B per store).
+//
+// Replaces the int4/int2 packing of RetrievalIndex.batch_append / append
+// (modules/kvr_retrieval.py:162-207) with the 1-bit tile codec.
+#include "kvr_common.h"
+
+namespace kvr {
+
+template <int DT, int TF, int T>
+__global__ __launch_bounds__(64) void encode_tiles_kernel(
+    const void* __restrict__ x, int64_t n_h, int64_t n_tiles, int64_t n_tok, int64_t stride_b,
+    int64_t stride_h, int64_t stride_t, uint64_t* __restrict__ bits, uint16_t* __restrict__ scales,
+    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg) {
+  constexpr int LDW = T + 1;  // padded row: conflict-free column writes and row reads
+  constexpr int W = T / 64;
+  __shared__ float ys[D * LDW];
+
+  const int lane = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int64_t seg = blk / n_tiles;
+  const int64_t tile = blk - seg * n_tiles;
+  const int64_t b = seg / n_h;
+  const int64_t h = seg - b * n_h;
+
+  // ---------------- phase A: lane = token
+#pragma unroll 1
+  for (int p = 0; p < W; ++p) {
+    const int t = p * 64 + lane;
+    const int64_t tok = tile * T + t;
+    const int64_t base = b * stride_b + h * stride_h + tok * stride_t;
+    float v[D];
+    if constexpr (DT == KVR_FP32) {
+      const float4* src = (const float4*)((const float*)x + base);
+#pragma unroll
+      for (int i = 0; i < D / 4; ++i) {
+        float4 f = src[i];
+        v[4 * i] = f.x;
+        v[4 * i + 1] = f.y;
+        v[4 * i + 2] = f.z;
+        v[4 * i + 3] = f.w;
+      }
+    } else {
+      const uint4* src = (const uint4*)((const uint16_t*)x + base);
+#pragma unroll
+      for (int i = 0; i < D / 8; ++i) {
+        uint4 r = src[i];
+        uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if constexpr (DT == KVR_BF16) {
+            v[8 * i + 2 * k] = __uint_as_float(w4[k] << 16);
+            v[8 * i + 2 * k + 1] = __uint_as_float(w4[k] & 0xffff0000u);
+          } else {
+            v[8 * i + 2 * k] = f16_to_f32(w4[k] & 0xffffu);
+            v[8 * i + 2 * k + 1] = f16_to_f32(w4[k] >> 16);
+          }
+        }
+      }
+    }
+    float* drow = dbg ? dbg + (seg * n_tok + tok) * D : nullptr;
+    if constexpr (TF == KVR_DCT) {
+#pragma unroll 1
+      for (int k = 0; k < D; ++k) {
+        const float* c = g_dct + k * D;
+        float acc = 0.f;
+#pragma unroll
+        for (int n = 0; n < D; ++n) acc = fmaf(c[n], v[n], acc);
+        ys[k * LDW + t] = acc;
+        if (drow) drow[k] = acc;
+      }
+    } else {
+      if constexpr (TF == KVR_HADAMARD) {
+        fwht128_regs(v);
+#pragma unroll
+        for (int j = 0; j < D; ++j) v[j] = v[j] * C_HAD;
+      }
+#pragma unroll
+      for (int j = 0; j < D; ++j) ys[j * LDW + t] = v[j];
+      if (drow) {
+        float4* d4 = (float4*)drow;
+#pragma unroll
+        for (int i = 0; i < D / 4; ++i) d4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---------------- phase B: lane = channels (lane, lane + 64)
+  const float* y0 = ys + lane * LDW;
+  const float* y1 = ys + (lane + 64) * LDW;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll 8
+  for (int t = 0; t < T; ++t) {
+    s0 = s0 + fabsf(y0[t]);
+    s1 = s1 + fabsf(y1[t]);
+  }
+  float a = s0 + s1;  // tree step j += j + 64
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) a = a + shfl_xor_f(a, m);
+  float mean = a * (1.0f / (float)(T * D));
+  mean = (mean < FP16_MAX) ? mean : FP16_MAX;
+  const uint32_t s16 = f32_to_f16_rne(mean);
+  const float s32 = f16_to_f32(s16);
+
+  uint32_t w0[2 * W], w1[2 * W];
+#pragma unroll
+  for (int i = 0; i < 2 * W; ++i) {
+    w0[i] = 0u;
+    w1[i] = 0u;
+  }
+  float e0 = 0.f, e1 = 0.f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    float u0 = y0[t] + e0;
+    float u1 = y1[t] + e1;
+    bool b0 = u0 >= 0.f;
+    bool b1 = u1 >= 0.f;
+    e0 = u0 - (b0 ? s32 : -s32);
+    e1 = u1 - (b1 ? s32 : -s32);
+    w0[t >> 5] |= (uint32_t)b0 << (t & 31);
+    w1[t >> 5] |= (uint32_t)b1 << (t & 31);
+  }
+
+  const int64_t slot = seg * out_tile_stride + out_tile_offset + tile;
+  uint64_t* out = bits + slot * (int64_t)(D * W);
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    out[lane * W + w] = ((uint64_t)w0[2 * w + 1] << 32) | w0[2 * w];
+    out[(lane + 64) * W + w] = ((uint64_t)w1[2 * w + 1] << 32) | w1[2 * w];
+  }
+  if (lane == 0) scales[slot] = (uint16_t)s16;
+}
+
+template <int DT, int TF>
+static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h, int64_t n_tok,
+                                  int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
+                                  uint16_t* scales, int64_t ots, int64_t oto, float* dbg,
+                                  hipStream_t s) {
+  const int64_t n_tiles = n_tok / T;
+  const int64_t nblk = n_b * n_h * n_tiles;
+  if (nblk == 0) return hipSuccess;
+  dim3 grid((unsigned)nblk), block(64);
+  if (T == 64)
+    hipLaunchKernelGGL((encode_tiles_kernel<DT, TF, 64>), grid, block, 0, s, x, n_h, n_tiles, n_tok,
+                       sb, sh, st, bits, scales, ots, oto, dbg);
+  else
+    hipLaunchKernelGGL((encode_tiles_kernel<DT, TF, 128>), grid, block, 0, s, x, n_h, n_tiles,
+                       n_tok, sb, sh, st, bits, scales, ots, oto, dbg);
+  return hipGetLastError();
+}
+
+hipError_t launch_encode(int dt, int tf, int T, const void* x, int64_t n_b, int64_t n_h,
+                         int64_t n_tok, int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
+                         uint16_t* scales, int64_t ots, int64_t oto, float* dbg, hipStream_t s) {
+#define KVR_ENC(DTV, TFV)                                                                       \
+  if (dt == DTV && tf == TFV)                                                                   \
+    return launch_encode_t<DTV, TFV>(T, x, n_b, n_h, n_tok, sb, sh, st, bits, scales, ots, oto, \
+                                     dbg, s);
+  KVR_ENC(KVR_BF16, KVR_HADAMARD)
+  KVR_ENC(KVR_FP16, KVR_HADAMARD)
+  KVR_ENC(KVR_FP32, KVR_HADAMARD)
+  KVR_ENC(KVR_BF16, KVR_DCT)
+  KVR_ENC(KVR_FP16, KVR_DCT)
+  KVR_ENC(KVR_FP32, KVR_DCT)
+  KVR_ENC(KVR_FP32, KVR_NONE)
+#undef KVR_ENC
+  return hipErrorInvalidValue;
+}
+
+}  // namespace kvr

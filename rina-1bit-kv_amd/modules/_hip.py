@@ -1,0 +1,237 @@
+"""ctypes binding of libkvr_hip.so (the C ABI in include/kvr_capi.h).
+
+The HIP library is the only implementation of the hot path: if it is missing or
+no GPU is present these functions raise; there is no CPU fallback.  Tensors are
+PyTorch-ROCm device tensors used as plain memory; every call is launched on
+torch's current stream and returns without synchronising.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+BF16, FP16, FP32 = 0, 1, 2
+HADAMARD, DCT, NONE = 0, 1, 2
+TRANSFORMS = {"hadamard": HADAMARD, "dct": DCT, "none": NONE}
+_DT = {torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32}
+_TORCH_DT = {BF16: torch.bfloat16, FP16: torch.float16, FP32: torch.float32}
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkvr_hip.so")
+ABI_VERSION = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_Z = ctypes.c_size_t
+
+# name -> (restype, argtypes); the single source of the Python-side signatures.
+SIGNATURES = {
+    "kvr_abi_version": (_I, []),
+    "kvr_last_error": (ctypes.c_char_p, []),
+    "kvr_encode_tiles": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _P, _L, _L, _P, _P]),
+    "kvr_query_prep": (_I, [_P, _I, _L, _I, _I, _I, _I, _P, _P, _P]),
+    "kvr_score_tiles": (_I, [_P, _P, _L, _L, _L, _I, _I, _P, _P, _I, _P, _P]),
+    "kvr_topk_tiles": (_I, [_P, _L, _L, _L, _I, _P, _P]),
+    "kvr_decode_attn_workspace": (_Z, [_L, _I, _I, _L, _I, _I]),
+    "kvr_decode_attn": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _P, _P, _P, _P,
+                             _L, _I, _I, _P, _I, _P, _I, _P, _Z, _P]),
+    "kvr_decode_step_workspace": (_Z, [_L, _I, _I, _L, _L, _I, _I]),
+    "kvr_decode_step": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _P, _P, _P, _P,
+                             _L, _L, _I, _I, _P, _P, _I, _P, _I, _P, _P, _Z, _P]),
+    "kvr_gather_tiles": (_I, [_P, _P, _L, _L, _I, _I, _P, _I, _P, _L, _L, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libkvr_hip.so once (after torch, so both share one HIP runtime)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `make -C rina-1bit-kv_amd/csrc` or "
+                "`python -c 'import __graft_entry__ as g; g.build()'` (no CPU fallback exists)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        if handle.kvr_abi_version() != ABI_VERSION:
+            raise RuntimeError("libkvr_hip.so ABI version mismatch; rebuild it")
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().kvr_last_error().decode()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("kvr HIP kernels need device tensors (no CPU fallback)")
+
+
+def tiles_words(T: int) -> int:
+    return T // 64
+
+
+def alloc_store(n_seg: int, tile_cap: int, T: int, device) -> tuple:
+    """(bits int64 [n_seg, tile_cap, 128, T/64], scales fp16 [n_seg, tile_cap]) zero-filled."""
+    bits = torch.zeros((n_seg, tile_cap, 128, T // 64), dtype=torch.int64, device=device)
+    scales = torch.zeros((n_seg, tile_cap), dtype=torch.float16, device=device)
+    return bits, scales
+
+
+# ----------------------------------------------------------------------------- encode
+
+def encode_tiles(x: torch.Tensor, T: int, transform: int, bits=None, scales=None, tile_offset: int = 0,
+                 want_rotated: bool = False):
+    """Encode x [n_b, n_h, n_tok, 128] (last dim contiguous, any other strides) into 1-bit tiles.
+
+    Writes tiles [tile_offset, tile_offset + n_tok/T) of each segment b*n_h+h of the store
+    (bits [n_b*n_h, cap, 128, T/64] int64, scales [n_b*n_h, cap] fp16), allocating a
+    store of exactly n_tok/T tiles when none is given.  Returns (bits, scales[, rotated]).
+    """
+    _require_gpu(x)
+    if x.dim() != 4 or x.shape[-1] != 128 or x.stride(-1) != 1:
+        raise ValueError("x must be [n_b, n_h, n_tok, 128] with a contiguous last dim")
+    n_b, n_h, n_tok, _ = x.shape
+    if n_tok % T:
+        raise ValueError(f"n_tok={n_tok} is not a multiple of T={T}")
+    n_tiles = n_tok // T
+    if bits is None:
+        bits, scales = alloc_store(n_b * n_h, tile_offset + n_tiles, T, x.device)
+    rot = torch.empty((n_b * n_h, n_tok, 128), dtype=torch.float32, device=x.device) if want_rotated else None
+    sb, sh, st, _ = x.stride()
+    rc = lib().kvr_encode_tiles(_ptr(x), _DT[x.dtype], n_b, n_h, n_tok, sb, sh, st, 128, T, transform,
+                                _ptr(bits), _ptr(scales), bits.shape[1], tile_offset, _ptr(rot), _stream())
+    check(rc, "kvr_encode_tiles")
+    return (bits, scales, rot) if want_rotated else (bits, scales)
+
+
+# ----------------------------------------------------------------------------- query / score / top-k
+
+def query_prep(q: torch.Tensor, n_kv: int, transform: int, want_q_rot: bool = True):
+    """q [B, Hq, 128] -> (qbar_rot [B*Hkv, 128] fp32, q_rot [B*Hq, 128] fp32 or None)."""
+    _require_gpu(q)
+    q = q.contiguous()
+    B, Hq, _ = q.shape
+    qbar = torch.empty((B * n_kv, 128), dtype=torch.float32, device=q.device)
+    qrot = torch.empty((B * Hq, 128), dtype=torch.float32, device=q.device) if want_q_rot else None
+    rc = lib().kvr_query_prep(_ptr(q), _DT[q.dtype], B, Hq, n_kv, 128, transform, _ptr(qbar), _ptr(qrot),
+                              _stream())
+    check(rc, "kvr_query_prep")
+    return qbar, qrot
+
+
+def score_tiles(qbar_rot: torch.Tensor, kbits: torch.Tensor, n_tiles: int, T: int, excl_lo=None,
+                excl_hi=None, method: int = 0, out=None):
+    """Scores [BH, n_tiles] fp32 of the first n_tiles tiles of each segment."""
+    _require_gpu(qbar_rot, kbits)
+    BH = kbits.shape[0]
+    if out is None:
+        out = torch.empty((BH, n_tiles), dtype=torch.float32, device=kbits.device)
+    rc = lib().kvr_score_tiles(_ptr(qbar_rot.contiguous()), _ptr(kbits), BH, n_tiles, kbits.shape[1], 128,
+                               T, _ptr(excl_lo), _ptr(excl_hi), method, _ptr(out), _stream())
+    check(rc, "kvr_score_tiles")
+    return out
+
+
+def topk_tiles(scores: torch.Tensor, k: int, out=None):
+    """idx [BH, k] int32: score descending, ties by tile index ascending."""
+    _require_gpu(scores)
+    BH, n = scores.shape
+    if out is None:
+        out = torch.empty((BH, k), dtype=torch.int32, device=scores.device)
+    rc = lib().kvr_topk_tiles(_ptr(scores), BH, n, scores.stride(0), k, _ptr(out), _stream())
+    check(rc, "kvr_topk_tiles")
+    return out
+
+
+# ----------------------------------------------------------------------------- attention
+
+def _window_args(win_k, win_v, win_len):
+    if win_k is None or win_len == 0:
+        return None, None, BF16, 0, 0, 0, 0
+    if win_k.stride() != win_v.stride() or win_k.stride(-1) != 1:
+        raise ValueError("window K and V need identical strides and a contiguous last dim")
+    sb, sh, st, _ = win_k.stride()
+    return win_k, win_v, _DT[win_k.dtype], win_len, sb, sh, st
+
+
+def decode_attn(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, idx, T, transform,
+                out_dtype=torch.float32, workspace=None):
+    """Fused window + retrieved-tile attention.  q [B, Hq, 128]; window [B, Hkv, W, 128]."""
+    _require_gpu(q, win_k, kbits, idx)
+    q = q.contiguous()
+    B, Hq, _ = q.shape
+    Hkv = win_k.shape[1] if win_k is not None else kbits.shape[0] // B
+    k = 0 if idx is None else idx.shape[1]
+    wk, wv, wdt, wl, sb, sh, st = _window_args(win_k, win_v, win_len)
+    need = lib().kvr_decode_attn_workspace(B, Hq, Hkv, wl, k, T)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)
+    out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
+    tile_stride = kbits.shape[1] if kbits is not None else 1
+    rc = lib().kvr_decode_attn(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, sb, sh, st,
+                               _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), tile_stride, T,
+                               transform, _ptr(idx), k, _ptr(out), _DT[out_dtype], _ptr(workspace),
+                               workspace.numel(), _stream())
+    check(rc, "kvr_decode_attn")
+    return out
+
+
+def decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T, device):
+    need = lib().kvr_decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T)
+    return torch.empty(max(need, 256), dtype=torch.uint8, device=device)
+
+
+def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles, T, transform, k,
+                excl_lo=None, excl_hi=None, out_dtype=torch.bfloat16, out=None, idx_out=None,
+                workspace=None):
+    """The whole decode hot path for one layer (query prep, scoring, top-k, attention)."""
+    _require_gpu(q)
+    q = q.contiguous()
+    B, Hq, _ = q.shape
+    Hkv = win_k.shape[1] if win_k is not None else kbits.shape[0] // B
+    wk, wv, wdt, wl, sb, sh, st = _window_args(win_k, win_v, win_len)
+    if workspace is None:
+        workspace = decode_step_workspace(B, Hq, Hkv, wl, n_tiles, k, T, q.device)
+    if out is None:
+        out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
+    tile_stride = kbits.shape[1] if kbits is not None else 1
+    rc = lib().kvr_decode_step(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, sb, sh, st,
+                               _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), n_tiles, tile_stride, T,
+                               transform, _ptr(excl_lo), _ptr(excl_hi), k, _ptr(out), _DT[out.dtype],
+                               _ptr(idx_out), _ptr(workspace), workspace.numel(), _stream())
+    check(rc, "kvr_decode_step")
+    return out
+
+
+def gather_tiles(bits, scales, idx, T, transform, out=None):
+    """Tokens of the selected tiles in the original domain: [BH, k*T, 128] fp32."""
+    _require_gpu(bits, idx)
+    BH, k = idx.shape
+    if out is None:
+        out = torch.empty((BH, k * T, 128), dtype=torch.float32, device=bits.device)
+    rc = lib().kvr_gather_tiles(_ptr(bits), _ptr(scales), BH, bits.shape[1], T, transform, _ptr(idx), k,
+                                _ptr(out), out.stride(0), out.stride(1), _stream())
+    check(rc, "kvr_gather_tiles")
+    return out
