@@ -76,7 +76,7 @@ template <int QT, int WDT, int QS, int PS>
 __global__ __launch_bounds__(WIN_THREADS) void window_attn_kernel(
     const void* __restrict__ q, int Hq, int Hkv, const uint16_t* __restrict__ wk,
     const uint16_t* __restrict__ wv, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
-    int64_t span, int n_parts, float* __restrict__ rec) {
+    int64_t span, int n_wparts, int n_parts, float* __restrict__ rec) {
   __shared__ __attribute__((aligned(16))) uint16_t vstage[4][WIN_CHUNK * VROW];
   __shared__ float cm[4][16], cl[4][16];
 
@@ -86,8 +86,8 @@ __global__ __launch_bounds__(WIN_THREADS) void window_attn_kernel(
   const int n = lane & 15;   // head column
   const int kg = lane >> 4;  // k-slot group
   const int g = Hq / Hkv;
-  const int64_t seg = blockIdx.x / n_parts;
-  const int part = (int)(blockIdx.x - seg * n_parts);
+  const int64_t seg = blockIdx.x / n_wparts;  // grid = segments x window parts
+  const int part = (int)(blockIdx.x - seg * n_wparts);
   const int64_t b = seg / Hkv;
   const int64_t h = seg - b * Hkv;
 
@@ -595,11 +595,11 @@ static hipError_t launch_window_t(bool f32out, const void* q, int64_t B, int Hq,
   if (f32out)
     hipLaunchKernelGGL((window_attn_kernel<QT, WDT, QS, 3>), grid, block, 0, s, q, Hq, Hkv,
                        (const uint16_t*)wk, (const uint16_t*)wv, win_len, sb, sh, st, p.span,
-                       n_parts, rec);
+                       p.n_wparts, n_parts, rec);
   else
     hipLaunchKernelGGL((window_attn_kernel<QT, WDT, QS, 2>), grid, block, 0, s, q, Hq, Hkv,
                        (const uint16_t*)wk, (const uint16_t*)wv, win_len, sb, sh, st, p.span,
-                       n_parts, rec);
+                       p.n_wparts, n_parts, rec);
   return hipGetLastError();
 }
 

@@ -282,8 +282,10 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_tiles_kernel(const float* _
     }
     if (gt) {
       const uint32_t p = atomicAdd(&sh_ngt, 1u);
-      sel_key[p] = key;
-      sel_idx[p] = (int32_t)i;
+      if (p < n_gt_total) {  // exactly n_gt_total keys exceed tau; never write past them
+        sel_key[p] = key;
+        sel_idx[p] = (int32_t)i;
+      }
     }
     const uint64_t bal = __ballot(eq);
     const uint32_t below = (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));

@@ -107,7 +107,7 @@ def test_encode_edge_tiles(H):
     T = 64
     x = np.zeros((1, 3, T, 128), np.float32)
     x[0, 1] = 0.37
-    x[0, 2] = 3.0e5
+    x[0, 2] = 1.0e7   # mean |y| = 1e7/sqrt(128) > fp16 max
     xt = torch.from_numpy(x).to(DEV, torch.bfloat16)
     bits, scales, rot = H.encode_tiles(xt, T, H.HADAMARD, want_rotated=True)
     torch.cuda.synchronize()
@@ -309,8 +309,12 @@ def test_decode_step_matches_oracle_pipeline(H, rng, tf, T, Hq, Hkv):
     wk = torch.from_numpy(kv_like(rng, (B, Hkv, W, 128))).to(DEV, torch.bfloat16)
     wv = torch.from_numpy(rng.standard_normal((B, Hkv, W, 128)).astype(np.float32)).to(DEV, torch.bfloat16)
     n_tiles = n_tok // T
-    lo = torch.tensor([0, 3, 0, 0, 1, 0, 0, 0][:B * Hkv], dtype=torch.int32, device=DEV)
-    hi = torch.tensor([0, 5, 0, 0, 2, 0, 0, 0][:B * Hkv], dtype=torch.int32, device=DEV)
+    lo_np = np.zeros(B * Hkv, np.int32)
+    hi_np = np.zeros(B * Hkv, np.int32)
+    lo_np[1], hi_np[1] = 3, 5          # exclude tiles 3..4 of segment 1
+    lo_np[-1], hi_np[-1] = 0, 1        # and tile 0 of the last segment
+    lo = torch.from_numpy(lo_np).to(DEV)
+    hi = torch.from_numpy(hi_np).to(DEV)
     idx = torch.empty((B * Hkv, k), dtype=torch.int32, device=DEV)
     out = H.decode_step(q, wk, wv, W, kb, vb, ks, vs, n_tiles, T, tf, k, excl_lo=lo, excl_hi=hi,
                         out_dtype=torch.float32, idx_out=idx)
