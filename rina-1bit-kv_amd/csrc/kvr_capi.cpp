@@ -21,13 +21,13 @@ hipError_t launch_score(int T, int method, const float* qbar_rot, const uint64_t
                         const int32_t* excl_hi, float* scores, hipStream_t s);
 hipError_t launch_topk(const float* scores, int64_t BH, int64_t n, int64_t stride, int k,
                        int32_t* idx, hipStream_t s);
-hipError_t launch_attention(int qt, const void* q, const float* q_rot, int64_t B, int Hq, int Hkv,
-                            const void* wk, const void* wv, int wdt, int64_t win_len, int64_t sb,
-                            int64_t sh, int64_t st, const uint64_t* kb, const uint64_t* vb,
-                            const uint16_t* ks, const uint16_t* vs, int64_t tile_stride, int T,
-                            int tf, const int32_t* idx, int k, void* out, int ot, float* rec,
-                            hipStream_t s);
-size_t attn_records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k);
+hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
+                         const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
+                         const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
+                         const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
+                         const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
+                         float* scores, int32_t* idx, float* rec, void* out, int ot, hipStream_t s);
+size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k);
 hipError_t launch_gather(const uint64_t* bits, const uint16_t* scales, int64_t BH,
                          int64_t tile_stride, int T, int tf, const int32_t* idx, int k, float* out,
                          int64_t oss, int64_t ost, hipStream_t s);
@@ -104,22 +104,19 @@ int check_store(const uint64_t* kb, const uint64_t* vb, const uint16_t* ks, cons
 }
 
 struct StepLayout {
-  size_t q_rot, qbar, scores, idx, rec, total;
+  size_t scores, idx, rec, total;
 };
 
+// Workspace: [scores | idx | partial records]; plain scratch, no state between calls.
 StepLayout step_layout(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles, int k) {
   StepLayout L{};
   size_t off = 0;
-  L.q_rot = off;
-  off += round_up((size_t)(B * Hq) * 128 * sizeof(float));
-  L.qbar = off;
-  off += round_up((size_t)(B * Hkv) * 128 * sizeof(float));
   L.scores = off;
   off += round_up((size_t)(B * Hkv) * (size_t)(n_tiles > 0 ? n_tiles : 0) * sizeof(float));
   L.idx = off;
   off += round_up((size_t)(B * Hkv) * (size_t)(k > 0 ? k : 0) * sizeof(int32_t));
   L.rec = off;
-  off += round_up(kvr::attn_records_bytes(B, Hq, Hkv, win_len, k));
+  off += round_up(kvr::records_bytes(B, Hq, Hkv, win_len, k));
   L.total = off;
   return L;
 }
@@ -252,17 +249,11 @@ int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                 workspace ? ws_bytes : (size_t)0);
   if (!aligned(workspace, kAlign)) return fail(KVR_ERR_ALIGN, "workspace must be 256-byte aligned");
   char* ws = (char*)workspace;
-  hipStream_t s = (hipStream_t)stream;
-  float* q_rot = (float*)(ws + L.q_rot);
-  float* qbar = (float*)(ws + L.qbar);
-  if (int r = hip_status(kvr::launch_query_prep(q_dtype, transform, q, B, Hq, Hkv, qbar,
-                                                k > 0 ? q_rot : nullptr, s),
-                         "kvr_decode_attn/query_prep"))
-    return r;
-  return hip_status(kvr::launch_attention(q_dtype, q, q_rot, B, Hq, Hkv, win_k, win_v, win_dtype,
-                                          win_len, win_stride_b, win_stride_h, win_stride_t, kbits,
-                                          vbits, kscale, vscale, tile_stride, T, transform, idx, k,
-                                          out, out_dtype, (float*)(ws + L.rec), s),
+  return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
+                                       win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
+                                       kscale, vscale, 0, tile_stride, T, transform, nullptr, nullptr,
+                                       k, false, nullptr, const_cast<int32_t*>(idx),
+                                       (float*)(ws + L.rec), out, out_dtype, (hipStream_t)stream),
                     "kvr_decode_attn");
 }
 
@@ -299,30 +290,13 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                 workspace ? ws_bytes : (size_t)0);
   if (!aligned(workspace, kAlign)) return fail(KVR_ERR_ALIGN, "workspace must be 256-byte aligned");
   char* ws = (char*)workspace;
-  hipStream_t s = (hipStream_t)stream;
-  float* q_rot = (float*)(ws + L.q_rot);
-  float* qbar = (float*)(ws + L.qbar);
-  float* scores = (float*)(ws + L.scores);
   int32_t* idx = idx_out ? idx_out : (int32_t*)(ws + L.idx);
-  const int64_t BH = B * Hkv;
-  if (int r = hip_status(kvr::launch_query_prep(q_dtype, transform, q, B, Hq, Hkv, qbar,
-                                                k > 0 ? q_rot : nullptr, s),
-                         "kvr_decode_step/query_prep"))
-    return r;
-  if (k > 0) {
-    if (int r = hip_status(kvr::launch_score(T, 0, qbar, kbits, BH, n_tiles, tile_stride, excl_lo,
-                                             excl_hi, scores, s),
-                           "kvr_decode_step/score"))
-      return r;
-    if (int r = hip_status(kvr::launch_topk(scores, BH, n_tiles, n_tiles, k, idx, s),
-                           "kvr_decode_step/topk"))
-      return r;
-  }
-  return hip_status(kvr::launch_attention(q_dtype, q, q_rot, B, Hq, Hkv, win_k, win_v, win_dtype,
-                                          win_len, win_stride_b, win_stride_h, win_stride_t, kbits,
-                                          vbits, kscale, vscale, tile_stride, T, transform, idx, k,
-                                          out, out_dtype, (float*)(ws + L.rec), s),
-                    "kvr_decode_step/attention");
+  return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
+                                       win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
+                                       kscale, vscale, n_tiles, tile_stride, T, transform, excl_lo,
+                                       excl_hi, k, true, (float*)(ws + L.scores), idx,
+                                       (float*)(ws + L.rec), out, out_dtype, (hipStream_t)stream),
+                    "kvr_decode_step");
 }
 
 int kvr_gather_tiles(const uint64_t* bits, const uint16_t* scales, int64_t BH, int64_t tile_stride,

@@ -63,38 +63,89 @@ __device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int m) {
   return (uint32_t)__shfl_xor((int)v, m, 64);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
+// Cross-lane moves without LDS: DPP inside 16-lane rows, v_permlane{16,32}_swap
+// across rows (gfx950).  xor16 / xor32 return the value of lane ^ 16 / lane ^ 32.
+#define KVR_DPP(v, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xf, 0xf, false))
+__device__ __forceinline__ float xor16_f(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32_f(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
+// Row (16-lane) reductions: xor 1, xor 2 (quad_perm), then half-mirror and mirror,
+// after which every lane of the row holds the row's result.
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, KVR_DPP(v, 0xb1));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, KVR_DPP(v, 0x4e));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, KVR_DPP(v, 0x141));  // row_half_mirror
+  v = fmaxf(v, KVR_DPP(v, 0x140));  // row_mirror
   return v;
+}
+__device__ __forceinline__ float row_sum(float v) {
+  v = v + KVR_DPP(v, 0xb1);
+  v = v + KVR_DPP(v, 0x4e);
+  v = v + KVR_DPP(v, 0x141);
+  v = v + KVR_DPP(v, 0x140);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row_max(v);
+  v = fmaxf(v, xor16_f(v));
+  return fmaxf(v, xor32_f(v));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = v + shfl_xor_f(v, m);
-  return v;
+  v = row_sum(v);
+  v = v + xor16_f(v);
+  return v + xor32_f(v);
 }
 
-// One FWHT butterfly stage across lanes for a value held one-per-lane:
-// lanes with (lane & m) == 0 hold the lower element of each pair.
-// Lower: a + b; upper: a - b (a = lower value, b = upper value) -- the same
-// single fp32 add/sub the oracle performs.
-__device__ __forceinline__ float fwht_xlane(float v, int lane, int m) {
-  float p = shfl_xor_f(v, m);
-  return (lane & m) ? (p - v) : (v + p);
+// Value of lane ^ M for a compile-time M (no LDS): quad_perm for 1, 2; half-mirror
+// then quad-reverse for 4; row_ror:8 for 8; permlane swaps for 16, 32.  All 64
+// lanes must be active.
+template <int M>
+__device__ __forceinline__ float xor_lane_f(float v) {
+  if constexpr (M == 1) return KVR_DPP(v, 0xb1);
+  else if constexpr (M == 2) return KVR_DPP(v, 0x4e);
+  else if constexpr (M == 4) return KVR_DPP(KVR_DPP(v, 0x141), 0x1b);
+  else if constexpr (M == 8) return KVR_DPP(v, 0x128);
+  else if constexpr (M == 16) return xor16_f(v);
+  else return xor32_f(v);
+}
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane_u(uint32_t v) {
+  return __float_as_uint(xor_lane_f<M>(__uint_as_float(v)));
+}
+
+// One FWHT butterfly stage across lanes for a value held one-per-lane: lanes with
+// (lane & M) == 0 hold the lower element of each pair.  Lower: a + b; upper: a - b
+// (a = lower value, b = upper value) -- the same single fp32 add/sub the oracle does.
+template <int M>
+__device__ __forceinline__ float fwht_xlane(float v, int lane) {
+  const float p = xor_lane_f<M>(v);
+  return (lane & M) ? (p - v) : (v + p);
 }
 
 // Full orthonormal Hadamard-128 (spec order h = 1..64, then * C_HAD) of a
 // vector held as channels (2*lane, 2*lane+1) in (v0, v1).  Bit-exact.
 __device__ __forceinline__ void hadamard_pair(float& v0, float& v1, int lane) {
   float a = v0 + v1, b = v0 - v1;  // h = 1
-  v0 = a;
-  v1 = b;
-#pragma unroll
-  for (int m = 1; m <= 32; m <<= 1) {  // h = 2m: partner lane = lane ^ m
-    v0 = fwht_xlane(v0, lane, m);
-    v1 = fwht_xlane(v1, lane, m);
-  }
+  v0 = fwht_xlane<1>(a, lane);     // h = 2m: partner lane = lane ^ m
+  v1 = fwht_xlane<1>(b, lane);
+  v0 = fwht_xlane<2>(v0, lane);
+  v1 = fwht_xlane<2>(v1, lane);
+  v0 = fwht_xlane<4>(v0, lane);
+  v1 = fwht_xlane<4>(v1, lane);
+  v0 = fwht_xlane<8>(v0, lane);
+  v1 = fwht_xlane<8>(v1, lane);
+  v0 = fwht_xlane<16>(v0, lane);
+  v1 = fwht_xlane<16>(v1, lane);
+  v0 = fwht_xlane<32>(v0, lane);
+  v1 = fwht_xlane<32>(v1, lane);
   v0 = v0 * C_HAD;
   v1 = v1 * C_HAD;
 }

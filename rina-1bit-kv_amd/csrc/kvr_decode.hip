@@ -1,0 +1,1450 @@
+// Subsystems 2-4 of the compressed-KV decode path on gfx950: query preparation,
+// tile scoring, top-k tile selection, fused window + retrieved-tile attention,
+// the log-sum-exp merge, and the materialising tile gather.
+//
+// One decode step (kvr_decode_step) is three launches and no block ever waits for
+// another block inside a launch (an agent-scope fence costs an L2 write-back on
+// gfx950, so cross-block hand-offs inside a kernel are avoided):
+//   score   : one item per (segment, 64 tiles); the block rotates the segment's
+//             GQA-mean query itself and writes fp32 scores.  (segment = sequence x
+//             KV head)
+//   attend  : window items (128 window tokens of one segment, MFMA) interleaved with
+//             retrieved items (4 selected tiles of one segment, one per wave, VALU
+//             bit-unpack); a retrieved item first selects its segment's top-k from
+//             the scores (every item of the segment computes the same selection).
+//             Both write partial softmax records.
+//   merge   : log-sum-exp merge of a segment's records, inverse rotation of the
+//             retrieved part, output.
+//
+// Partial records: per segment s and part p, g*(2+128) floats: m2[g] (running max,
+// log2 units), l[g], o[g][128].  Window parts hold o in the original domain,
+// retrieved parts in the rotated domain (rotated back once per head in the merge).
+//
+// Reference behaviour followed (Misaka477/RINA-1bit-KV):
+//   GQA mean query          modules/kvr_retrieval.py:270, 296
+//   chunk-mean cosine score modules/kvr_retrieval.py:291-315 (+1e-8 on both norms)
+//   NaN -> -inf, exclusion  modules/kvr_retrieval.py:287-288, 373-377, 391
+//   per-KV-head top-k       modules/kvr_retrieval.py:379, 392
+//   joint softmax, 1/sqrt(d) modules/kvr_hook.py:274-282; online form of
+//                            modules/kvr_triton.py:56-79
+#include <cstdlib>
+
+#include "kvr_common.h"
+
+namespace kvr {
+
+constexpr int NT = 256;           // threads per block (4 waves) for every decode role
+constexpr int SCORE_TILES = 64;   // tiles per score item (16 groups x 4)
+constexpr int WIN_SPAN = 512;     // window tokens per window item (4 waves x 4 chunks of 32)
+constexpr int WIN_CHUNK = 32;
+constexpr int VROW = D + 8;       // bf16 elements per staged V row (16 B pad)
+constexpr int TOPK_MAX_K = 1024;
+constexpr float SCALE_LOG2 = 0.08838834764831845f * LOG2E;  // log2(e) / sqrt(128)
+
+struct DecodeArgs {
+  const void* q;
+  int q_dtype, Hq, Hkv, g, transform, out_dtype;
+  const uint16_t* wk;
+  const uint16_t* wv;
+  int64_t win_len, sb, sh, st;
+  const uint64_t* kbits;
+  const uint64_t* vbits;
+  const uint16_t* kscale;
+  const uint16_t* vscale;
+  int64_t n_tiles, tile_stride;
+  const int32_t* excl_lo;
+  const int32_t* excl_hi;
+  int k;
+  float* scores;      // [BH][n_tiles]
+  int32_t* idx;       // [BH][k]
+  float* rec;         // [BH][n_parts][g][2+D]
+  int n_chunks, n_wparts, n_rparts;
+  int do_select;      // retrieved items select their tiles from scores (else read idx)
+  int ret_method;     // retrieved tiles: 0 = MFMA on unpacked +-1 operands, 1 = VALU nibble tables
+  void* out;          // [B][Hq][D]
+};
+
+// ------------------------------------------------------------------ small helpers
+
+__device__ __forceinline__ float q_elem(const DecodeArgs& a, int64_t i) {
+  if (a.q_dtype == KVR_BF16) return load_as_f32<KVR_BF16>(a.q, i);
+  if (a.q_dtype == KVR_FP16) return load_as_f32<KVR_FP16>(a.q, i);
+  return load_as_f32<KVR_FP32>(a.q, i);
+}
+
+// LDS in-order completion within one wave (no block barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ void rotate_pair(float& v0, float& v1, int lane, int tf, float* xs) {
+  if (tf == KVR_HADAMARD) hadamard_pair(v0, v1, lane);
+  else if (tf == KVR_DCT) dct_pair(v0, v1, lane, xs);
+}
+
+__device__ __forceinline__ void unrotate_pair(float& v0, float& v1, int lane, int tf, float* xs) {
+  if (tf == KVR_HADAMARD) hadamard_pair(v0, v1, lane);  // orthonormal and symmetric
+  else if (tf == KVR_DCT) idct_pair(v0, v1, lane, xs);
+}
+
+// Rotated GQA-mean query of one segment into qs[128] (one wave; lane = channels
+// 2*lane, 2*lane+1).  fp32 sum in head order, one correctly rounded division.
+__device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs, int lane) {
+  const int64_t b = seg / a.Hkv;
+  const int h = (int)(seg - b * a.Hkv);
+  const int64_t q0 = (b * a.Hq + (int64_t)h * a.g) * D;
+  float m0 = q_elem(a, q0 + 2 * lane), m1 = q_elem(a, q0 + 2 * lane + 1);
+  for (int i = 1; i < a.g; ++i) {
+    m0 = m0 + q_elem(a, q0 + (int64_t)i * D + 2 * lane);
+    m1 = m1 + q_elem(a, q0 + (int64_t)i * D + 2 * lane + 1);
+  }
+  m0 = __fdiv_rn(m0, (float)a.g);
+  m1 = __fdiv_rn(m1, (float)a.g);
+  rotate_pair(m0, m1, lane, a.transform, xs);
+  qs[2 * lane] = m0;
+  qs[2 * lane + 1] = m1;
+}
+
+// ------------------------------------------------------------------ scoring
+
+template <int METHOD>
+__device__ __forceinline__ int count_bits(uint64_t w) {
+  if constexpr (METHOD == 0) {
+    return __popcll(w);  // v_bcnt_u32_b32 x 2
+  } else {               // SWAR bit-unpack: pairwise bit sums, same count
+    uint64_t x = w - ((w >> 1) & 0x5555555555555555ull);
+    x = (x & 0x3333333333333333ull) + ((x >> 2) & 0x3333333333333333ull);
+    x = (x + (x >> 4)) & 0x0f0f0f0f0f0f0f0full;
+    return (int)((x * 0x0101010101010101ull) >> 56);
+  }
+}
+
+// 16-lane tree h = 8, 4, 2, 1 (every lane of the group ends with the same value).
+__device__ __forceinline__ float tree16(float p) {
+  p = p + shfl_xor_f(p, 8);
+  p = p + shfl_xor_f(p, 4);
+  p = p + shfl_xor_f(p, 2);
+  p = p + shfl_xor_f(p, 1);
+  return p;
+}
+
+// Score tiles [t0, t1) of one segment.  16 lanes per tile, lane li owns channels
+// 8li..8li+7: per-lane sequential fp32 sum of fl(q*c), then the 16-lane tree.
+template <int T, int METHOD>
+__device__ void score_tiles_block(const float* qs, const uint64_t* kbits, int64_t seg, int64_t n_tiles,
+                                  int64_t tile_stride, int64_t t0, int64_t t1, int32_t lo, int32_t hi,
+                                  float* scores) {
+  constexpr int W = T / 64;
+  const int tid = threadIdx.x;
+  const int grp = tid >> 4;
+  const int li = tid & 15;
+  float q[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) q[k] = qs[8 * li + k];
+  float qq = q[0] * q[0];
+#pragma unroll
+  for (int k = 1; k < 8; ++k) qq = qq + q[k] * q[k];
+  qq = tree16(qq);
+  const float qn = sqrt_rn(qq) + EPS;
+  const uint64_t* segbits = kbits + seg * tile_stride * (int64_t)(D * W);
+  for (int64_t tile = t0 + grp; tile < t1; tile += 16) {
+    const uint64_t* wp = segbits + tile * (D * W) + 8 * li * W;
+    uint64_t wd[8 * W];
+#pragma unroll
+    for (int i = 0; i < 4 * W; ++i) {
+      ulonglong2 v = ((const ulonglong2*)wp)[i];
+      wd[2 * i] = v.x;
+      wd[2 * i + 1] = v.y;
+    }
+    float dot = 0.f;
+    int cc = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      int pc = 0;
+#pragma unroll
+      for (int w = 0; w < W; ++w) pc += count_bits<METHOD>(wd[k * W + w]);
+      const int c = 2 * pc - T;
+      cc += c * c;
+      const float prod = q[k] * (float)c;
+      dot = (k == 0) ? prod : dot + prod;
+    }
+    dot = tree16(dot);
+    cc += __shfl_xor(cc, 8, 64);
+    cc += __shfl_xor(cc, 4, 64);
+    cc += __shfl_xor(cc, 2, 64);
+    cc += __shfl_xor(cc, 1, 64);
+    if (li == 0) {
+      const float cn = sqrt_rn((float)cc) + EPS;
+      float sc = __fdiv_rn(dot, qn * cn);
+      if (sc != sc) sc = -__builtin_inff();
+      if (tile >= lo && tile < hi) sc = -__builtin_inff();
+      scores[seg * n_tiles + tile] = sc;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ top-k (one wave)
+
+struct TopkSmem {
+  uint32_t hist[256];
+  uint32_t selk[TOPK_MAX_K];
+  int32_t seli[TOPK_MAX_K];
+};
+
+// Writes the k winners (key, index) into sm.selk / sm.seli in index order of the
+// two classes (keys > tau first, then the first kk keys == tau), then rank-sorts
+// them by (key desc, index asc) into out[0..k).
+__device__ void topk_rank_out(int k, int32_t* out, TopkSmem& sm, int lane) {
+  wave_lds_sync();
+  for (int ai = lane; ai < k; ai += 64) {
+    const uint32_t ka = sm.selk[ai];
+    const int32_t ia = sm.seli[ai];
+    int rank = 0;
+    for (int bi = 0; bi < k; ++bi) {
+      const uint32_t kb = sm.selk[bi];
+      const int32_t ib = sm.seli[bi];
+      rank += (kb > ka) || (kb == ka && ib < ia);
+    }
+    out[rank] = ia;
+  }
+}
+
+// Register-resident select for n <= 64*KPL: bitwise (MSB-first) search of tau, the
+// largest key with #{key >= tau} >= k, by wave ballots; no LDS atomics.
+template <int KPL>
+__device__ void topk_wave_regs(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
+  uint32_t key[KPL];
+#pragma unroll
+  for (int r = 0; r < KPL; ++r) {
+    const int64_t i = (int64_t)r * 64 + lane;
+    key[r] = (i < n) ? score_key(row[i]) : 0u;  // padding sorts below every score (even -inf)
+  }
+  uint32_t tau = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int r = 0; r < KPL; ++r) cnt += __popcll(__ballot(key[r] >= cand));
+    if (cnt >= k) tau = cand;
+  }
+  int n_gt = 0;
+#pragma unroll
+  for (int r = 0; r < KPL; ++r) n_gt += __popcll(__ballot(key[r] > tau));
+  const int kk = k - n_gt;
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  int cg = 0, ce = 0;
+#pragma unroll
+  for (int r = 0; r < KPL; ++r) {  // slot r covers indices 64r..64r+63 in lane order
+    const bool gt = key[r] > tau, eq = key[r] == tau;
+    const uint64_t bg = __ballot(gt), be = __ballot(eq);
+    const int i = r * 64 + lane;
+    if (gt) {
+      const int p = cg + __popcll(bg & lt_mask);
+      sm.selk[p] = key[r];
+      sm.seli[p] = i;
+    }
+    if (eq) {
+      const int q = ce + __popcll(be & lt_mask);
+      if (q < kk) {
+        sm.selk[n_gt + q] = key[r];
+        sm.seli[n_gt + q] = i;
+      }
+    }
+    cg += __popcll(bg);
+    ce += __popcll(be);
+  }
+  topk_rank_out(k, out, sm, lane);
+}
+
+// Any n: 4 x 8-bit radix passes with an LDS histogram, keys re-read from row.
+__device__ void topk_wave_hist(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
+  uint32_t prefix = 0, pmask = 0, kk = (uint32_t)k;
+#pragma unroll 1
+  for (int shift = 24; shift >= 0; shift -= 8) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.hist[lane + 64 * r] = 0;
+    wave_lds_sync();
+    for (int64_t i = lane; i < n; i += 64) {
+      const uint32_t key = score_key(row[i]);
+      if ((key & pmask) == prefix) atomicAdd(&sm.hist[(key >> shift) & 255u], 1u);
+    }
+    wave_lds_sync();
+    uint32_t c[4], tot = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // lane owns bins 255-4*lane .. 252-4*lane
+      c[r] = sm.hist[255 - 4 * lane - r];
+      tot += c[r];
+    }
+    uint32_t incl = tot;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, m, 64);
+      if (lane >= m) incl += o;
+    }
+    const uint32_t excl = incl - tot;
+    uint32_t digit = 0, nkk = 0;
+    const bool mine = excl < kk && kk <= incl;
+    if (mine) {
+      uint32_t run = excl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (run < kk && kk <= run + c[r] && nkk == 0) {
+          digit = 255u - 4u * lane - r;
+          nkk = kk - run;
+        }
+        run += c[r];
+      }
+    }
+    const int src = (int)__builtin_ctzll(__ballot(mine));  // exactly one lane owns the k-th key
+    digit = (uint32_t)__shfl((int)digit, src, 64);
+    kk = (uint32_t)__shfl((int)nkk, src, 64);
+    prefix |= digit << shift;
+    pmask |= 255u << shift;
+  }
+  const uint32_t tau = prefix;
+  const uint32_t n_gt = (uint32_t)k - kk;
+  uint32_t cnt_gt = 0, cnt_eq = 0;
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+#pragma unroll 1
+  for (int64_t c0 = 0; c0 < n; c0 += 64) {
+    const int64_t i = c0 + lane;
+    const uint32_t key = (i < n) ? score_key(row[i]) : 0u;
+    const bool gt = (i < n) && key > tau;
+    const bool eq = (i < n) && key == tau;
+    const uint64_t bg = __ballot(gt), be = __ballot(eq);
+    if (gt) {
+      const uint32_t p = cnt_gt + (uint32_t)__popcll(bg & lt_mask);
+      if (p < n_gt) {
+        sm.selk[p] = key;
+        sm.seli[p] = (int32_t)i;
+      }
+    }
+    if (eq) {
+      const uint32_t r = cnt_eq + (uint32_t)__popcll(be & lt_mask);
+      if (r < kk) {
+        sm.selk[n_gt + r] = key;
+        sm.seli[n_gt + r] = (int32_t)i;
+      }
+    }
+    cnt_gt += (uint32_t)__popcll(bg);
+    cnt_eq += (uint32_t)__popcll(be);
+    if (cnt_gt >= n_gt && cnt_eq >= kk) break;  // uniform across the wave
+  }
+  topk_rank_out(k, out, sm, lane);
+}
+
+// idx[0..k) = indices of the k largest scores of row[0..n), score descending then
+// index ascending (NaN counts as -inf).
+__device__ void topk_wave(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
+  if (n <= 512) topk_wave_regs<8>(row, n, k, out, sm, lane);
+  else if (n <= 1024) topk_wave_regs<16>(row, n, k, out, sm, lane);
+  else if (n <= 2048) topk_wave_regs<32>(row, n, k, out, sm, lane);
+  else topk_wave_hist(row, n, k, out, sm, lane);
+}
+
+// ------------------------------------------------------------------ MFMA helpers
+
+template <int WDT>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (WDT == KVR_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Split an fp32 value into NS 16-bit parts of the MFMA input type whose sum
+// reproduces it to ~8*NS mantissa bits (bf16: truncation, exact remainders;
+// fp16: round to nearest).
+template <int WDT, int NS>
+__device__ __forceinline__ void split16(float x, uint32_t* part) {
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    if constexpr (WDT == KVR_BF16) {
+      const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+      part[i] = hb >> 16;
+      x = x - __uint_as_float(hb);
+    } else {
+      const _Float16 hh = (_Float16)x;
+      part[i] = (uint32_t)__builtin_bit_cast(uint16_t, hh);
+      x = x - (float)hh;
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) { return lo16 | (hi16 << 16); }
+
+// Combine per-wave softmax partials of one block into a record.  Each wave
+// holds (m_w, l_w) per head column and o contributions; ost is LDS [16][128].
+struct CombineSmem {
+  float cm[4][16];
+  float cl[4][16];
+};
+
+__device__ void write_record_stats(const CombineSmem& cs, float* R, int g, int tid) {
+  if (tid < g) {
+    float mh = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mh = fmaxf(mh, cs.cm[w][tid]);
+    const float muh = (mh == -__builtin_inff()) ? 0.f : mh;
+    float lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) lt += cs.cl[w][tid] * exp2f(cs.cm[w][tid] - muh);
+    R[tid] = mh;
+    R[g + tid] = lt;
+  }
+}
+
+// ------------------------------------------------------------------ window role (MFMA)
+
+struct WindowSmem {
+  union {
+    uint16_t vstage[4][WIN_CHUNK * VROW];  // per-wave V staging
+    float ost[16 * D];                      // combine buffer (after the main loop)
+  };
+  CombineSmem cs;
+};
+
+// S^T[16 tok x 16 heads] = K[16 x 32 dims] Q^T[32 x 16];  O^T[16 dims x 16 heads] +=
+// V^T[16 dims x 32 tok] P^T[32 tok x 16 heads].  Lane (n = lane & 15, kg = lane >> 4):
+// Q^T/P^T column n = head n; S^T rows 4kg..4kg+3 of a 16-token block are tokens
+// 16 tb + 4kg + r, which is the k-slot (kg, e = 4 tb + r) of the PV product, so the
+// probabilities feed the B operand in place.  Block i of O^T has row m <-> dim 8m+i.
+template <int WDT, int QS, int PS>
+__device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv_id = tid >> 6;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  const int g = a.g;
+  const int64_t b = seg / a.Hkv;
+  const int64_t h = seg - b * a.Hkv;
+
+  u32x4 qb[QS][4];
+  {
+    const int64_t qoff = (b * a.Hq + h * g + n) * D;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint32_t pe[QS][8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (n < g) ? q_elem(a, qoff + 32 * ks + 8 * kg + e) : 0.f;
+        uint32_t p[QS];
+        split16<WDT, QS>(x, p);
+#pragma unroll
+        for (int sp = 0; sp < QS; ++sp) pe[sp][e] = p[sp];
+      }
+#pragma unroll
+      for (int sp = 0; sp < QS; ++sp)
+        qb[sp][ks] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
+                           pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
+    }
+  }
+
+  f32x4 oacc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+
+  const uint16_t* kbase = a.wk + b * a.sb + h * a.sh;
+  const uint16_t* vbase = a.wv + b * a.sb + h * a.sh;
+  const int64_t win_len = a.win_len, st = a.st;
+  const int64_t t_begin = (int64_t)part * WIN_SPAN;
+  const int64_t t_end = (t_begin + WIN_SPAN < win_len) ? t_begin + WIN_SPAN : win_len;
+  uint16_t* vs = sm.vstage[wv_id];
+
+  for (int64_t c0 = t_begin + (int64_t)wv_id * WIN_CHUNK; c0 < t_end; c0 += 4 * WIN_CHUNK) {
+    u32x4 ka[2][4];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      int64_t tok = c0 + 16 * tb + n;
+      tok = tok < win_len ? tok : win_len - 1;
+      const uint16_t* kr = kbase + tok * st + 8 * kg;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) ka[tb][ks] = *(const u32x4*)(kr + 32 * ks);
+    }
+    u32x4 vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int64_t tok = c0 + 4 * i + kg;
+      tok = tok < win_len ? tok : win_len - 1;
+      vr[i] = *(const u32x4*)(vbase + tok * st + 8 * n);
+    }
+    f32x4 s[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      s[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int sp = 0; sp < QS; ++sp) s[tb] = mfma16<WDT>(ka[tb][ks], qb[sp][ks], s[tb]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *(u32x4*)(vs + (4 * i + kg) * VROW + 8 * n) = vr[i];
+
+    float l2[8];
+    float cmax = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t tok = c0 + 16 * (e >> 2) + 4 * kg + (e & 3);
+      float v = s[e >> 2][e & 3] * SCALE_LOG2;
+      v = (tok < t_end) ? v : -__builtin_inff();
+      l2[e] = v;
+      cmax = fmaxf(cmax, v);
+    }
+    cmax = fmaxf(cmax, xor16_f(cmax));
+    cmax = fmaxf(cmax, xor32_f(cmax));
+    const float m_new = fmaxf(m_run, cmax);
+    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    m_run = m_new;
+    float p[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = exp2f(l2[e] - m_use);
+      psum += p[e];
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) oacc[i] = oacc[i] * alpha;
+    u32x4 pb[PS];
+    {
+      uint32_t pe[PS][8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t pp[PS];
+        split16<WDT, PS>(p[e], pp);
+#pragma unroll
+        for (int sp = 0; sp < PS; ++sp) pe[sp][e] = pp[sp];
+      }
+#pragma unroll
+      for (int sp = 0; sp < PS; ++sp)
+        pb[sp] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
+                       pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
+    }
+    wave_lds_sync();
+    u32x4 rv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int trow = 16 * (e >> 2) + 4 * kg + (e & 3);
+      rv[e] = *(const u32x4*)(vs + trow * VROW + 8 * n);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+      u32x4 av;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) av[j] = __builtin_amdgcn_perm(rv[2 * j + 1][i >> 1], rv[2 * j][i >> 1], sel);
+#pragma unroll
+      for (int sp = 0; sp < PS; ++sp) oacc[i] = mfma16<WDT>(av, pb[sp], oacc[i]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  l_run += xor16_f(l_run);
+  l_run += xor32_f(l_run);
+  if (kg == 0) {
+    sm.cs.cm[wv_id][n] = m_run;
+    sm.cs.cl[wv_id][n] = l_run;
+  }
+  __syncthreads();
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm.cs.cm[w][n]);
+  const float fw = exp2f(m_run - ((mx == -__builtin_inff()) ? 0.f : mx));
+  for (int i = tid; i < 16 * D; i += NT) sm.ost[i] = 0.f;
+  __syncthreads();
+#pragma unroll 1
+  for (int w = 0; w < 4; ++w) {
+    if (wv_id == w && n < g) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sm.ost[n * D + 32 * kg + 8 * r + i] += oacc[i][r] * fw;
+    }
+    __syncthreads();
+  }
+  const int n_parts = a.n_wparts + a.n_rparts;
+  float* R = a.rec + (seg * n_parts + part) * (int64_t)(g * (2 + D));
+  write_record_stats(sm.cs, R, g, tid);
+  for (int i = tid; i < g * D; i += NT) R[2 * g + i] = sm.ost[i];
+}
+
+// ------------------------------------------------------------------ retrieved role (VALU)
+
+// 64x64 bit-matrix transpose across the wave: lane l holds row l (bit c = element
+// (l, c)); afterwards lane c holds column c (bit l = element (l, c)).  Six block-swap
+// stages; lane exchanges by v_permlane32_swap / permlane16 / DPP (no LDS).
+template <int S>
+__device__ __forceinline__ uint32_t tstage(uint32_t x, int lane, uint32_t m) {
+  const uint32_t p = xor_lane_u<S>(x);
+  return (lane & S) ? ((x & ~m) | ((p >> S) & m)) : ((x & m) | ((p & m) << S));
+}
+
+__device__ __forceinline__ void transpose64(uint32_t& lo, uint32_t& hi, int lane) {
+  {
+    // stage 32: lower lanes take the partner's lo as hi, upper lanes its hi as lo
+    const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+    lo = r[0];
+    hi = r[1];
+  }
+  lo = tstage<16>(lo, lane, 0x0000ffffu);
+  hi = tstage<16>(hi, lane, 0x0000ffffu);
+  lo = tstage<8>(lo, lane, 0x00ff00ffu);
+  hi = tstage<8>(hi, lane, 0x00ff00ffu);
+  lo = tstage<4>(lo, lane, 0x0f0f0f0fu);
+  hi = tstage<4>(hi, lane, 0x0f0f0f0fu);
+  lo = tstage<2>(lo, lane, 0x33333333u);
+  hi = tstage<2>(hi, lane, 0x33333333u);
+  lo = tstage<1>(lo, lane, 0x55555555u);
+  hi = tstage<1>(hi, lane, 0x55555555u);
+}
+
+template <int G4>
+struct RetSmem {
+  int32_t sel[TOPK_MAX_K];    // the segment's selected tiles (score desc, index asc)
+  float lq[32 * 16 * G4];     // [channel nibble][pattern][head]: sums of q'
+  float qs[G4 * D];           // rotated query heads of the segment
+  float qsum[G4];
+  float xs[4][D];             // per-wave scratch of the DCT helpers
+  CombineSmem cs;
+  union {
+    TopkSmem tk;                // selection (before the tile loop)
+    struct {
+      float lu[4][16 * 16 * G4];  // per wave [token nibble][pattern][head]: sums of p
+      float ps[4][64 * G4];       // per wave [token][head]
+    } t;                        // tile loop
+    float ost[16 * D];          // combine (after the tile loop)
+  } u;
+};
+
+template <int W>
+struct TileWords {
+  uint64_t k0[W], k1[W], v0[W], v1[W];
+  float sk, sv;
+};
+
+template <int T>
+__device__ __forceinline__ void load_tile(const DecodeArgs& a, int64_t seg, int64_t tile, int lane,
+                                          TileWords<T / 64>& tw) {
+  constexpr int W = T / 64;
+  tile = tile < 0 ? 0 : (tile >= a.tile_stride ? a.tile_stride - 1 : tile);  // stay inside the store
+  const int64_t slot = seg * a.tile_stride + tile;
+  const uint64_t* kp = a.kbits + slot * (int64_t)(D * W);
+  const uint64_t* vp = a.vbits + slot * (int64_t)(D * W);
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    tw.k0[w] = kp[lane * W + w];
+    tw.k1[w] = kp[(lane + 64) * W + w];
+    tw.v0[w] = vp[lane * W + w];
+    tw.v1[w] = vp[(lane + 64) * W + w];
+  }
+  tw.sk = f16_to_f32(a.kscale[slot]);
+  tw.sv = f16_to_f32(a.vscale[slot]);
+}
+
+// All selected tiles of one segment in one block: wave w takes tiles w, w+4, ...
+// (the next tile's words are loaded while the current one is processed).  Keys /
+// values of a retrieved token are s*(2b-1) per rotated channel.  Logits:
+// dot_h(t) = sum_j q'_hj b_tj from the nibble table of q' applied to the transposed
+// token rows; PV: sum_t p_ht b_tj from a per-tile nibble table of p applied to the
+// channel words.  The 4 waves' online-softmax partials are combined into one record.
+template <int T, int G4>
+__device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem<G4>& sm) {
+  constexpr int W = T / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv_id = tid >> 6;
+  const int g = a.g;
+  const int k = a.k;
+  const int64_t b = seg / a.Hkv;
+  const int64_t h = seg - b * a.Hkv;
+  const int RS = a.n_rparts;
+
+  // wave 0 selects the tiles (when asked) while the other waves rotate query heads
+  const int qw0 = a.do_select ? 1 : 0;
+  if (a.do_select && wv_id == 0) {
+    topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sm.sel, sm.u.tk, lane);
+    wave_lds_sync();
+    if (rp == 0)
+      for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.sel[i];
+  }
+  if (wv_id >= qw0) {
+    for (int hh = wv_id - qw0; hh < G4; hh += 4 - qw0) {
+      float v0 = 0.f, v1 = 0.f;
+      if (hh < g) {
+        const int64_t qo = (b * a.Hq + h * g + hh) * D;
+        v0 = q_elem(a, qo + 2 * lane);
+        v1 = q_elem(a, qo + 2 * lane + 1);
+        rotate_pair(v0, v1, lane, a.transform, sm.xs[wv_id]);
+      }
+      sm.qs[hh * D + 2 * lane] = v0;
+      sm.qs[hh * D + 2 * lane + 1] = v1;
+      const float tot = wave_sum(v0 + v1);
+      if (lane == 0) sm.qsum[hh] = tot;
+    }
+  }
+  __syncthreads();
+  for (int ent = tid; ent < 32 * 16; ent += NT) {
+    const int c4 = ent >> 4, e = ent & 15;
+#pragma unroll
+    for (int hh = 0; hh < G4; ++hh) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (e & (1 << i)) acc += sm.qs[hh * D + 4 * c4 + i];
+      sm.lq[ent * G4 + hh] = acc;
+    }
+  }
+  TileWords<W> cur, nxt;
+  const int j0 = rp * 4 + wv_id;
+  if (j0 < k) load_tile<T>(a, seg, a.do_select ? sm.sel[j0] : a.idx[seg * k + j0], lane, cur);
+  __syncthreads();
+
+  float m_run[G4], l_lane[G4], o0[G4], o1[G4];
+#pragma unroll
+  for (int hh = 0; hh < G4; ++hh) {
+    m_run[hh] = -__builtin_inff();
+    l_lane[hh] = 0.f;
+    o0[hh] = 0.f;
+    o1[hh] = 0.f;
+  }
+  float* lu = sm.u.t.lu[wv_id];
+  float* ps = sm.u.t.ps[wv_id];
+#pragma unroll 1
+  for (int j = j0; j < k; j += 4 * RS) {
+    if (j + 4 * RS < k)
+      load_tile<T>(a, seg, a.do_select ? sm.sel[j + 4 * RS] : a.idx[seg * k + j + 4 * RS], lane, nxt);
+#pragma unroll 1
+    for (int w = 0; w < W; ++w) {
+      uint32_t a_lo = (uint32_t)cur.k0[w], a_hi = (uint32_t)(cur.k0[w] >> 32);
+      uint32_t b_lo = (uint32_t)cur.k1[w], b_hi = (uint32_t)(cur.k1[w] >> 32);
+      transpose64(a_lo, a_hi, lane);  // token row, channels 0..63
+      transpose64(b_lo, b_hi, lane);  // token row, channels 64..127
+      float dot[G4];
+#pragma unroll
+      for (int hh = 0; hh < G4; ++hh) dot[hh] = 0.f;
+#pragma unroll
+      for (int c4 = 0; c4 < 32; ++c4) {
+        const uint32_t word = (c4 < 8) ? a_lo : (c4 < 16) ? a_hi : (c4 < 24) ? b_lo : b_hi;
+        const uint32_t e = (word >> (4 * (c4 & 7))) & 15u;
+        const float* ent = sm.lq + (c4 * 16 + e) * G4;
+#pragma unroll
+        for (int hh = 0; hh < G4; hh += 4) {
+          const float4 v = *(const float4*)(ent + hh);
+          dot[hh] += v.x;
+          dot[hh + 1] += v.y;
+          dot[hh + 2] += v.z;
+          dot[hh + 3] += v.w;
+        }
+      }
+      float alpha[G4], psum[G4];
+#pragma unroll
+      for (int hh = 0; hh < G4; ++hh) {
+        const float lg = cur.sk * (2.f * dot[hh] - sm.qsum[hh]) * SCALE_LOG2;
+        const float m_new = fmaxf(m_run[hh], wave_max(lg));
+        alpha[hh] = exp2f(m_run[hh] - m_new);
+        m_run[hh] = m_new;
+        const float p = exp2f(lg - m_new);
+        l_lane[hh] = l_lane[hh] * alpha[hh] + p;
+        psum[hh] = wave_sum(p);
+        ps[lane * G4 + hh] = p;
+      }
+      wave_lds_sync();
+      for (int ent = lane; ent < 16 * 16; ent += 64) {
+        const int tn = ent >> 4, e = ent & 15;
+#pragma unroll
+        for (int hh = 0; hh < G4; ++hh) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (e & (1 << i)) acc += ps[(4 * tn + i) * G4 + hh];
+          lu[ent * G4 + hh] = acc;
+        }
+      }
+      wave_lds_sync();
+      float x0[G4], x1[G4];
+#pragma unroll
+      for (int hh = 0; hh < G4; ++hh) {
+        x0[hh] = 0.f;
+        x1[hh] = 0.f;
+      }
+      const uint32_t vv[4] = {(uint32_t)cur.v0[w], (uint32_t)(cur.v0[w] >> 32), (uint32_t)cur.v1[w],
+                              (uint32_t)(cur.v1[w] >> 32)};
+#pragma unroll
+      for (int tn = 0; tn < 16; ++tn) {
+        const uint32_t e0 = (vv[tn >> 3] >> (4 * (tn & 7))) & 15u;
+        const uint32_t e1 = (vv[2 + (tn >> 3)] >> (4 * (tn & 7))) & 15u;
+        const float* t0 = lu + (tn * 16 + e0) * G4;
+        const float* t1 = lu + (tn * 16 + e1) * G4;
+#pragma unroll
+        for (int hh = 0; hh < G4; hh += 4) {
+          const float4 p0 = *(const float4*)(t0 + hh);
+          const float4 p1 = *(const float4*)(t1 + hh);
+          x0[hh] += p0.x; x0[hh + 1] += p0.y; x0[hh + 2] += p0.z; x0[hh + 3] += p0.w;
+          x1[hh] += p1.x; x1[hh + 1] += p1.y; x1[hh + 2] += p1.z; x1[hh + 3] += p1.w;
+        }
+      }
+#pragma unroll
+      for (int hh = 0; hh < G4; ++hh) {
+        o0[hh] = o0[hh] * alpha[hh] + cur.sv * (2.f * x0[hh] - psum[hh]);
+        o1[hh] = o1[hh] * alpha[hh] + cur.sv * (2.f * x1[hh] - psum[hh]);
+      }
+      wave_lds_sync();  // ps / lu are rewritten by the next sub-tile
+    }
+    cur = nxt;
+  }
+
+  // combine the 4 waves (head hh of wave w: m_run[hh], l = wave sum of l_lane)
+#pragma unroll
+  for (int hh = 0; hh < G4; ++hh) {
+    const float lt = wave_sum(l_lane[hh]);
+    if (lane == 0) {
+      sm.cs.cm[wv_id][hh] = m_run[hh];
+      sm.cs.cl[wv_id][hh] = lt;
+    }
+  }
+  __syncthreads();  // every wave is past its last use of lu / ps
+  for (int i = tid; i < 16 * D; i += NT) sm.u.ost[i] = 0.f;
+  __syncthreads();
+#pragma unroll 1
+  for (int w = 0; w < 4; ++w) {
+    if (wv_id == w) {
+#pragma unroll
+      for (int hh = 0; hh < G4; ++hh) {
+        if (hh < g) {
+          float mx = -__builtin_inff();
+#pragma unroll
+          for (int w2 = 0; w2 < 4; ++w2) mx = fmaxf(mx, sm.cs.cm[w2][hh]);
+          const float fw = exp2f(m_run[hh] - ((mx == -__builtin_inff()) ? 0.f : mx));
+          sm.u.ost[hh * D + lane] += o0[hh] * fw;
+          sm.u.ost[hh * D + lane + 64] += o1[hh] * fw;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int n_parts = a.n_wparts + a.n_rparts;
+  float* R = a.rec + (seg * n_parts + a.n_wparts + rp) * (int64_t)(g * (2 + D));
+  write_record_stats(sm.cs, R, g, tid);
+  for (int i = tid; i < g * D; i += NT) R[2 * g + i] = sm.u.ost[i];
+}
+
+// ------------------------------------------------------------------ retrieved role (MFMA)
+
+struct RetMfmaSmem {
+  int32_t sel[TOPK_MAX_K];
+  u32x4 pm1[256];             // byte -> 8 fp16 values (+1 for a set bit, -1 otherwise)
+  u32x4 qb[4][2][64];         // Q'^T operands per k-step and fp16 part, per lane
+  float qs[16 * D];           // rotated query heads (zero beyond g)
+  float xs[4][D];
+  CombineSmem cs;
+  union {
+    TopkSmem tk;
+    float ost[16 * D];
+  } u;
+};
+
+__device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                0, 0, 0);
+}
+
+// Retrieved tiles of one segment on MFMA (fp16 inputs, fp32 accumulate).  Block rs of
+// the segment's RS blocks: wave w takes tiles rs*4 + w, then + 4*RS, ...
+//   S^T[16 tok x 16 heads] = Khat[16 tok x 32 ch] Q'^T[32 ch x 16 heads]: Khat = +-1
+//     from the token rows (64x64 bit transpose, then the byte of the row holding the
+//     lane's 8 channels, fetched from the row's lane), Q' split in 2 fp16 parts.
+//   O'^T[16 ch x 16 heads] += Vhat^T[16 ch x 32 tok] (sv P)^T[32 tok x 16 heads]: the
+//     S^T accumulator slots are the PV k-slots (as in the window part); Vhat^T = +-1
+//     from two nibbles of the lane's channel word; sv*P split in 2 fp16 parts.
+template <int T>
+__device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm) {
+  constexpr int W = T / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv_id = tid >> 6;
+  const int n = lane & 15;   // head column / token or channel row
+  const int kg = lane >> 4;  // k-slot group
+  const int g = a.g;
+  const int k = a.k;
+  const int RS = a.n_rparts;
+  const int64_t b = seg / a.Hkv;
+  const int64_t h = seg - b * a.Hkv;
+
+  // wave 0 selects (when asked); waves 1..3 (or 0..3) rotate the query heads
+  const int qw0 = a.do_select ? 1 : 0;
+  if (a.do_select && wv_id == 0) {
+    topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sm.sel, sm.u.tk, lane);
+    wave_lds_sync();
+    if (rs == 0)
+      for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.sel[i];
+  }
+  if (wv_id >= qw0) {
+    for (int hh = wv_id - qw0; hh < 16; hh += 4 - qw0) {
+      float v0 = 0.f, v1 = 0.f;
+      if (hh < g) {
+        const int64_t qo = (b * a.Hq + h * g + hh) * D;
+        v0 = q_elem(a, qo + 2 * lane);
+        v1 = q_elem(a, qo + 2 * lane + 1);
+        rotate_pair(v0, v1, lane, a.transform, sm.xs[wv_id]);
+      }
+      sm.qs[hh * D + 2 * lane] = v0;
+      sm.qs[hh * D + 2 * lane + 1] = v1;
+    }
+  }
+  {  // +-1 patterns: entry x, element e = bit e of x
+    const int x = tid;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = ((x >> (2 * j)) & 1) ? 0x3c00u : 0xbc00u;      // fp16 +1 / -1
+      const uint32_t hi = ((x >> (2 * j + 1)) & 1) ? 0x3c00u : 0xbc00u;
+      w[j] = lo | (hi << 16);
+    }
+    sm.pm1[x] = u32x4{w[0], w[1], w[2], w[3]};
+  }
+  __syncthreads();
+
+  // Q'^T operands (B): lane (head n, kg), k-step ks: q'[n][32 ks + 8 kg + e], 2 fp16
+  // parts; wave w builds k-step w into LDS (read back per tile, saving registers)
+  {
+    const int ks = wv_id;
+    uint32_t pe[2][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t pp[2];
+      split16<KVR_FP16, 2>(sm.qs[n * D + 32 * ks + 8 * kg + e], pp);
+      pe[0][e] = pp[0];
+      pe[1][e] = pp[1];
+    }
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp)
+      sm.qb[ks][sp][lane] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
+                                  pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
+  }
+  __syncthreads();
+
+  f32x4 oacc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -__builtin_inff(), l_run = 0.f;
+
+  for (int j = rs * 4 + wv_id; j < k; j += 4 * RS) {
+    int64_t tile = a.do_select ? sm.sel[j] : a.idx[seg * k + j];
+    tile = tile < 0 ? 0 : (tile >= a.tile_stride ? a.tile_stride - 1 : tile);  // stay inside the store
+    const int64_t slot = seg * a.tile_stride + tile;
+    const uint64_t* kp = a.kbits + slot * (int64_t)(D * W);
+    const uint64_t* vp = a.vbits + slot * (int64_t)(D * W);
+    const float sk = f16_to_f32(a.kscale[slot]) * SCALE_LOG2;
+    const float sv = f16_to_f32(a.vscale[slot]);
+#pragma unroll 1
+    for (int w = 0; w < W; ++w) {
+      const uint64_t ka = kp[lane * W + w], kb = kp[(lane + 64) * W + w];
+      const uint32_t* vp32 = (const uint32_t*)vp;
+      uint32_t vw[8];  // dword 0 of the lane's channel words (tokens 0..31)
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) vw[cb] = vp32[2 * ((16 * cb + n) * W + w)];
+      uint32_t row[4] = {(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)kb, (uint32_t)(kb >> 32)};
+      transpose64(row[0], row[1], lane);  // lane t: token t, channels 0..63
+      transpose64(row[2], row[3], lane);  // channels 64..127
+
+      // ---- S^T = Khat Q'^T (log2 units after * sk)
+      f32x4 sacc[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        sacc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const uint32_t d = (uint32_t)__shfl((int)row[ks], 16 * tb + n, 64);
+          const u32x4 av = sm.pm1[(d >> (8 * kg)) & 255u];
+          sacc[tb] = mfma16_f16(av, sm.qb[ks][0][lane], sacc[tb]);
+          sacc[tb] = mfma16_f16(av, sm.qb[ks][1][lane], sacc[tb]);
+        }
+      }
+      // ---- online softmax over the 64 tokens (head n lane-local)
+      float lg[16];
+      float cmax = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        lg[e] = sacc[e >> 2][e & 3] * sk;
+        cmax = fmaxf(cmax, lg[e]);
+      }
+      cmax = fmaxf(cmax, xor16_f(cmax));
+      cmax = fmaxf(cmax, xor32_f(cmax));
+      const float m_new = fmaxf(m_run, cmax);
+      const float alpha = exp2f(m_run - m_new);
+      m_run = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        lg[e] = exp2f(lg[e] - m_new);
+        psum += lg[e];
+      }
+      l_run = l_run * alpha + psum;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) oacc[i] = oacc[i] * alpha;
+
+      // ---- O'^T += Vhat^T (sv P)^T, two k-steps of 32 tokens
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        u32x4 pb[2];
+        {
+          uint32_t pe[2][8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            uint32_t pp[2];
+            split16<KVR_FP16, 2>(lg[8 * ks2 + e] * sv, pp);
+            pe[0][e] = pp[0];
+            pe[1][e] = pp[1];
+          }
+#pragma unroll
+          for (int sp = 0; sp < 2; ++sp)
+            pb[sp] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
+                           pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
+        }
+        if (ks2 == 1) {  // dword 1 of the channel words (tokens 32..63)
+#pragma unroll
+          for (int cb = 0; cb < 8; ++cb) vw[cb] = vp32[2 * ((16 * cb + n) * W + w) + 1];
+        }
+        const int sh0 = 4 * kg;
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+          const uint32_t lo = (vw[cb] >> sh0) & 15u;
+          const uint32_t hi = (vw[cb] >> (sh0 + 16)) & 15u;
+          const u32x4 av = sm.pm1[lo | (hi << 4)];
+          oacc[cb] = mfma16_f16(av, pb[0], oacc[cb]);
+          oacc[cb] = mfma16_f16(av, pb[1], oacc[cb]);
+        }
+      }
+    }
+  }
+
+  // ---- combine the 4 waves into one record (o' in the rotated domain)
+  l_run += xor16_f(l_run);
+  l_run += xor32_f(l_run);
+  if (kg == 0) {
+    sm.cs.cm[wv_id][n] = m_run;
+    sm.cs.cl[wv_id][n] = l_run;
+  }
+  __syncthreads();  // also: wave 0's selection scratch is dead
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm.cs.cm[w][n]);
+  const float fw = exp2f(m_run - ((mx == -__builtin_inff()) ? 0.f : mx));
+  for (int i = tid; i < 16 * D; i += NT) sm.u.ost[i] = 0.f;
+  __syncthreads();
+#pragma unroll 1
+  for (int w = 0; w < 4; ++w) {
+    if (wv_id == w && n < g) {
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sm.u.ost[n * D + 16 * cb + 4 * kg + r] += oacc[cb][r] * fw;
+    }
+    __syncthreads();
+  }
+  const int n_parts = a.n_wparts + a.n_rparts;
+  float* R = a.rec + (seg * n_parts + a.n_wparts + rs) * (int64_t)(g * (2 + D));
+  write_record_stats(sm.cs, R, g, tid);
+  for (int i = tid; i < g * D; i += NT) R[2 * g + i] = sm.u.ost[i];
+}
+
+// ------------------------------------------------------------------ merge
+
+// One wave per (sequence, query head): LSE-merge every partial record of its segment
+// (window parts in the original domain, retrieved parts rotated), rotate the
+// retrieved sum back, normalise, store.  Lane p first holds part p's weight so the
+// record loads of all parts can be in flight together.
+__global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
+  constexpr int MAXP = 16;  // records loaded per batch (all in flight together)
+  __shared__ float xs[D];
+  const int lane = threadIdx.x;
+  const int g = a.g;
+  const int64_t bq = blockIdx.x;  // b * Hq + head
+  const int64_t b = bq / a.Hq;
+  const int hq = (int)(bq - b * a.Hq);
+  const int h = hq / g, i = hq - h * g;
+  const int64_t seg = b * a.Hkv + h;
+  const int n_parts = a.n_wparts + a.n_rparts;
+  const int64_t rs = g * (2 + D);
+  const float* R0 = a.rec + seg * n_parts * rs;
+
+  float M = -__builtin_inff(), L = 0.f, w0 = 0.f, w1 = 0.f, r0 = 0.f, r1 = 0.f;
+  for (int p0 = 0; p0 < n_parts; p0 += MAXP) {
+    float pm[MAXP], pl[MAXP];
+    float2 po[MAXP];
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {  // branch-free: clamp the part, mask its weight below
+      const int pc = (p0 + p < n_parts) ? p0 + p : n_parts - 1;
+      const float* R = R0 + pc * rs;
+      pm[p] = R[i];
+      pl[p] = R[g + i];
+      po[p] = *(const float2*)(R + 2 * g + i * D + 2 * lane);
+    }
+    float Mb = -__builtin_inff();
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) Mb = fmaxf(Mb, pm[p]);
+    const float Mn = fmaxf(M, Mb);
+    const float mu = (Mn == -__builtin_inff()) ? 0.f : Mn;
+    const float sc = exp2f(M - mu);
+    L *= sc;
+    w0 *= sc;
+    w1 *= sc;
+    r0 *= sc;
+    r1 *= sc;
+    M = Mn;
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const float f = (p0 + p < n_parts) ? exp2f(pm[p] - mu) : 0.f;
+      const bool win = p0 + p < a.n_wparts;
+      L += pl[p] * f;
+      w0 += win ? po[p].x * f : 0.f;
+      w1 += win ? po[p].y * f : 0.f;
+      r0 += win ? 0.f : po[p].x * f;
+      r1 += win ? 0.f : po[p].y * f;
+    }
+  }
+  if (a.n_rparts > 0) unrotate_pair(r0, r1, lane, a.transform, xs);
+  const float inv = (L > 0.f) ? 1.f / L : 0.f;
+  const float y0 = (w0 + r0) * inv, y1 = (w1 + r1) * inv;
+  const int64_t o = bq * D + 2 * lane;
+  if (a.out_dtype == KVR_FP32) {
+    ((float2*)a.out)[o >> 1] = make_float2(y0, y1);
+  } else {
+    ((uint32_t*)a.out)[o >> 1] = pack2(f32_to_bf16_rne(y0), f32_to_bf16_rne(y1));
+  }
+}
+
+// ------------------------------------------------------------------ kernels
+
+// Score items with the query computed in-block: grid = segments x chunks of 64 tiles.
+template <int T>
+__global__ __launch_bounds__(NT) void select_score_kernel(DecodeArgs a) {
+  __shared__ float qs[D];
+  __shared__ float xs[D];
+  const int64_t seg = blockIdx.x / a.n_chunks;
+  const int64_t chunk = blockIdx.x - seg * a.n_chunks;
+  if (threadIdx.x < 64) qbar_wave(a, seg, qs, xs, threadIdx.x);
+  __syncthreads();
+  const int64_t t0 = chunk * SCORE_TILES;
+  const int64_t t1 = (t0 + SCORE_TILES < a.n_tiles) ? t0 + SCORE_TILES : a.n_tiles;
+  const int32_t lo = a.excl_lo ? a.excl_lo[seg] : 0;
+  const int32_t hi = a.excl_hi ? a.excl_hi[seg] : 0;
+  score_tiles_block<T, 0>(qs, a.kbits, seg, a.n_tiles, a.tile_stride, t0, t1, lo, hi, a.scores);
+}
+
+// Blocks [0, BH*n_rparts) are the retrieved items (segment-major; the long ones, so
+// they start first); the rest are the window items.
+template <int T, int WDT, int QS, int RM, int G4>
+__global__ __launch_bounds__(NT, 4) void attend_kernel(DecodeArgs a, int64_t BH) {
+  __shared__ union {
+    WindowSmem win;
+    RetSmem<G4> ret;
+    RetMfmaSmem retm;
+  } sm;
+  const int64_t n_r = BH * a.n_rparts;
+  if ((int64_t)blockIdx.x < n_r) {
+    const int64_t seg = blockIdx.x / a.n_rparts;
+    const int rs = (int)(blockIdx.x - seg * a.n_rparts);
+    if constexpr (RM == 0) retrieved_role_mfma<T>(a, seg, rs, sm.retm);
+    else retrieved_role<T, G4>(a, seg, rs, sm.ret);
+  } else {
+    const int64_t it = blockIdx.x - n_r;
+    const int64_t seg = it / a.n_wparts;
+    window_role<WDT, QS, 3>(a, seg, (int)(it - seg * a.n_wparts), sm.win);
+  }
+}
+
+// Output of segments with neither window tokens nor retrieved tiles: zeros.
+__global__ __launch_bounds__(NT) void zero_out_kernel(DecodeArgs a, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return;
+  if (a.out_dtype == KVR_FP32) ((float*)a.out)[i] = 0.f;
+  else ((uint16_t*)a.out)[i] = 0;
+}
+
+// Standalone component kernels ------------------------------------------------
+
+template <int QT, int TF>
+__global__ __launch_bounds__(64) void query_prep_kernel(const void* __restrict__ q, int Hq, int Hkv,
+                                                        float* __restrict__ qbar_rot,
+                                                        float* __restrict__ q_rot) {
+  __shared__ float xs[D];
+  const int lane = threadIdx.x;
+  const int64_t seg = blockIdx.x;
+  const int64_t b = seg / Hkv;
+  const int h = (int)(seg - b * Hkv);
+  const int g = Hq / Hkv;
+  const int64_t q0 = (b * Hq + (int64_t)h * g) * D;
+  float m0 = load_as_f32<QT>(q, q0 + 2 * lane);
+  float m1 = load_as_f32<QT>(q, q0 + 2 * lane + 1);
+  for (int i = 1; i < g; ++i) {
+    m0 = m0 + load_as_f32<QT>(q, q0 + (int64_t)i * D + 2 * lane);
+    m1 = m1 + load_as_f32<QT>(q, q0 + (int64_t)i * D + 2 * lane + 1);
+  }
+  m0 = __fdiv_rn(m0, (float)g);
+  m1 = __fdiv_rn(m1, (float)g);
+  rotate_pair(m0, m1, lane, TF, xs);
+  qbar_rot[seg * D + 2 * lane] = m0;
+  qbar_rot[seg * D + 2 * lane + 1] = m1;
+  if (q_rot) {
+    for (int i = 0; i < g; ++i) {
+      float v0 = load_as_f32<QT>(q, q0 + (int64_t)i * D + 2 * lane);
+      float v1 = load_as_f32<QT>(q, q0 + (int64_t)i * D + 2 * lane + 1);
+      rotate_pair(v0, v1, lane, TF, xs);
+      q_rot[q0 + (int64_t)i * D + 2 * lane] = v0;
+      q_rot[q0 + (int64_t)i * D + 2 * lane + 1] = v1;
+    }
+  }
+}
+
+template <int T, int METHOD>
+__global__ __launch_bounds__(NT) void score_kernel(const float* __restrict__ qbar_rot,
+                                                   const uint64_t* __restrict__ kbits, int64_t n_tiles,
+                                                   int64_t tile_stride, int64_t n_chunks,
+                                                   const int32_t* __restrict__ excl_lo,
+                                                   const int32_t* __restrict__ excl_hi,
+                                                   float* __restrict__ scores) {
+  __shared__ float qs[D];
+  const int64_t seg = blockIdx.x / n_chunks;
+  const int64_t chunk = blockIdx.x - seg * n_chunks;
+  if (threadIdx.x < D) qs[threadIdx.x] = qbar_rot[seg * D + threadIdx.x];
+  __syncthreads();
+  const int64_t t0 = chunk * SCORE_TILES;
+  const int64_t t1 = (t0 + SCORE_TILES < n_tiles) ? t0 + SCORE_TILES : n_tiles;
+  score_tiles_block<T, METHOD>(qs, kbits, seg, n_tiles, tile_stride, t0, t1,
+                               excl_lo ? excl_lo[seg] : 0, excl_hi ? excl_hi[seg] : 0, scores);
+}
+
+__global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ scores, int64_t n,
+                                                  int64_t stride, int k, int32_t* __restrict__ idx) {
+  __shared__ TopkSmem sm;
+  const int64_t seg = blockIdx.x;
+  topk_wave(scores + seg * stride, n, k, idx + seg * k, sm, threadIdx.x);
+}
+
+template <int T, int TF>
+__global__ __launch_bounds__(64) void gather_tiles_kernel(const uint64_t* __restrict__ bits,
+                                                          const uint16_t* __restrict__ scales,
+                                                          int64_t tile_stride,
+                                                          const int32_t* __restrict__ idx, int k,
+                                                          float* __restrict__ out, int64_t oss,
+                                                          int64_t ost) {
+  constexpr int W = T / 64;
+  const int lane = threadIdx.x;
+  const int64_t blk = blockIdx.x;  // (seg * k + j) * W + w
+  const int w = (int)(blk % W);
+  const int64_t sj = blk / W;
+  const int64_t seg = sj / k;
+  const int j = (int)(sj - seg * k);
+  int64_t tile = idx[seg * k + j];
+  tile = tile < 0 ? 0 : (tile >= tile_stride ? tile_stride - 1 : tile);  // stay inside the store
+  const int64_t slot = seg * tile_stride + tile;
+  const float s = f16_to_f32(scales[slot]);
+  const uint64_t* wp = bits + slot * (int64_t)(D * W);
+  const uint64_t wa = wp[lane * W + w], wc = wp[(lane + 64) * W + w];
+  uint32_t a_lo = (uint32_t)wa, a_hi = (uint32_t)(wa >> 32), c_lo = (uint32_t)wc, c_hi = (uint32_t)(wc >> 32);
+  transpose64(a_lo, a_hi, lane);
+  transpose64(c_lo, c_hi, lane);
+  const uint32_t rows[4] = {a_lo, a_hi, c_lo, c_hi};
+  float v[D];
+#pragma unroll
+  for (int ch = 0; ch < D; ++ch) v[ch] = ((rows[ch >> 5] >> (ch & 31)) & 1u) ? s : -s;
+  float* dst = out + seg * oss + ((int64_t)j * T + 64 * w + lane) * ost;
+  if constexpr (TF == KVR_HADAMARD) {
+    fwht128_regs(v);
+#pragma unroll
+    for (int ch = 0; ch < D; ++ch) dst[ch] = v[ch] * C_HAD;
+  } else if constexpr (TF == KVR_DCT) {
+#pragma unroll 1
+    for (int n2 = 0; n2 < D; ++n2) {
+      float acc = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < D; ++kk) acc = fmaf(g_dct[kk * D + n2], v[kk], acc);
+      dst[n2] = acc;
+    }
+  } else {
+#pragma unroll
+    for (int ch = 0; ch < D; ++ch) dst[ch] = v[ch];
+  }
+}
+
+// ------------------------------------------------------------------ host launchers
+
+int n_window_parts(int64_t win_len) { return (win_len > 0) ? (int)((win_len + WIN_SPAN - 1) / WIN_SPAN) : 0; }
+constexpr int RET_TILES_PER_BLOCK = 16;  // selected tiles per retrieved item (4 per wave)
+int n_retrieved_parts(int k) { return (k > 0) ? (k + RET_TILES_PER_BLOCK - 1) / RET_TILES_PER_BLOCK : 0; }
+
+size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k) {
+  const int g = Hq / Hkv;
+  const int64_t parts = n_window_parts(win_len) + n_retrieved_parts(k);
+  return (size_t)(B * Hkv * (parts > 0 ? parts : 1) * g * (2 + D)) * sizeof(float);
+}
+
+hipError_t launch_query_prep(int qt, int tf, const void* q, int64_t B, int Hq, int Hkv,
+                             float* qbar_rot, float* q_rot, hipStream_t s) {
+  const int64_t nblk = B * Hkv;
+  if (nblk == 0) return hipSuccess;
+#define KVR_QP(QTV, TFV)                                                                        \
+  if (qt == QTV && tf == TFV) {                                                                 \
+    hipLaunchKernelGGL((query_prep_kernel<QTV, TFV>), dim3((unsigned)nblk), dim3(64), 0, s, q, Hq, \
+                       Hkv, qbar_rot, q_rot);                                                   \
+    return hipGetLastError();                                                                   \
+  }
+  KVR_QP(KVR_BF16, KVR_HADAMARD)
+  KVR_QP(KVR_FP16, KVR_HADAMARD)
+  KVR_QP(KVR_FP32, KVR_HADAMARD)
+  KVR_QP(KVR_BF16, KVR_DCT)
+  KVR_QP(KVR_FP16, KVR_DCT)
+  KVR_QP(KVR_FP32, KVR_DCT)
+  KVR_QP(KVR_BF16, KVR_NONE)
+  KVR_QP(KVR_FP16, KVR_NONE)
+  KVR_QP(KVR_FP32, KVR_NONE)
+#undef KVR_QP
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_score(int T, int method, const float* qbar_rot, const uint64_t* kbits, int64_t BH,
+                        int64_t n_tiles, int64_t tile_stride, const int32_t* excl_lo,
+                        const int32_t* excl_hi, float* scores, hipStream_t s) {
+  const int64_t n_chunks = (n_tiles + SCORE_TILES - 1) / SCORE_TILES;
+  const int64_t nblk = BH * n_chunks;
+  if (nblk == 0) return hipSuccess;
+#define KVR_SC(TV, MV)                                                                           \
+  if (T == TV && method == MV) {                                                                 \
+    hipLaunchKernelGGL((score_kernel<TV, MV>), dim3((unsigned)nblk), dim3(NT), 0, s, qbar_rot, kbits, \
+                       n_tiles, tile_stride, n_chunks, excl_lo, excl_hi, scores);                \
+    return hipGetLastError();                                                                    \
+  }
+  KVR_SC(64, 0)
+  KVR_SC(64, 1)
+  KVR_SC(128, 0)
+  KVR_SC(128, 1)
+#undef KVR_SC
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_topk(const float* scores, int64_t BH, int64_t n, int64_t stride, int k, int32_t* idx,
+                       hipStream_t s) {
+  if (BH == 0) return hipSuccess;
+  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)BH), dim3(64), 0, s, scores, n, stride, k, idx);
+  return hipGetLastError();
+}
+
+// Retrieved-tile arithmetic: MFMA on unpacked +-1 operands (default) or the VALU
+// nibble-table path; KVR_RETRIEVE_METHOD=valu selects the latter (same results
+// within the attention tolerance).
+static int retrieve_method() {
+  const char* e = getenv("KVR_RETRIEVE_METHOD");
+  return (e && (e[0] == 'v' || e[0] == 'V')) ? 1 : 0;
+}
+
+// Full decode: [score launch when do_select] -> attend launch -> merge launch.
+hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
+                         const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
+                         const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
+                         const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
+                         const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
+                         float* scores, int32_t* idx, float* rec, void* out, int ot, hipStream_t s) {
+  DecodeArgs a{};
+  a.q = q;
+  a.q_dtype = qt;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.g = Hq / Hkv;
+  a.transform = tf;
+  a.out_dtype = ot;
+  a.wk = (const uint16_t*)wk;
+  a.wv = (const uint16_t*)wv;
+  a.win_len = win_len;
+  a.sb = sb;
+  a.sh = sh;
+  a.st = st;
+  a.kbits = kb;
+  a.vbits = vb;
+  a.kscale = ks;
+  a.vscale = vs;
+  a.n_tiles = n_tiles;
+  a.tile_stride = tile_stride;
+  a.excl_lo = excl_lo;
+  a.excl_hi = excl_hi;
+  a.k = k;
+  a.scores = scores;
+  a.idx = idx;
+  a.rec = rec;
+  a.n_chunks = (int)((n_tiles + SCORE_TILES - 1) / SCORE_TILES);
+  a.n_wparts = n_window_parts(win_len);
+  a.n_rparts = n_retrieved_parts(k);
+  a.do_select = (do_select && k > 0) ? 1 : 0;
+  a.ret_method = retrieve_method();
+  a.out = out;
+  const int64_t BH = B * Hkv;
+  if (BH == 0) return hipSuccess;
+  if (a.n_wparts + a.n_rparts == 0) {
+    const int64_t n = B * Hq * D;
+    hipLaunchKernelGGL(zero_out_kernel, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, a, n);
+    return hipGetLastError();
+  }
+  if (a.do_select) {
+    const dim3 grid((unsigned)(BH * a.n_chunks));
+    if (T == 64) hipLaunchKernelGGL(select_score_kernel<64>, grid, dim3(NT), 0, s, a);
+    else hipLaunchKernelGGL(select_score_kernel<128>, grid, dim3(NT), 0, s, a);
+    if (hipError_t e = hipGetLastError()) return e;
+  }
+  {
+    const dim3 grid((unsigned)(BH * (a.n_wparts + a.n_rparts)));
+    const bool same = (qt == wdt) || win_len == 0;
+    const int g = a.g;
+    const int gsel = (g <= 4) ? 4 : (g <= 8) ? 8 : 16;
+#define KVR_ATT(TV, WV, QSV, RMV, G4V) \
+  hipLaunchKernelGGL((attend_kernel<TV, WV, QSV, RMV, G4V>), grid, dim3(NT), 0, s, a, BH)
+#define KVR_ATT_G(TV, WV, QSV)                        \
+  if (a.ret_method == 0) KVR_ATT(TV, WV, QSV, 0, 4);  \
+  else if (gsel == 4) KVR_ATT(TV, WV, QSV, 1, 4);     \
+  else if (gsel == 8) KVR_ATT(TV, WV, QSV, 1, 8);     \
+  else KVR_ATT(TV, WV, QSV, 1, 16);
+#define KVR_ATT_Q(TV, WV) \
+  if (same) { KVR_ATT_G(TV, WV, 1) } else { KVR_ATT_G(TV, WV, 3) }
+    if (T == 64 && wdt == KVR_FP16) { KVR_ATT_Q(64, KVR_FP16) }
+    else if (T == 64) { KVR_ATT_Q(64, KVR_BF16) }
+    else if (wdt == KVR_FP16) { KVR_ATT_Q(128, KVR_FP16) }
+    else { KVR_ATT_Q(128, KVR_BF16) }
+#undef KVR_ATT_Q
+#undef KVR_ATT_G
+#undef KVR_ATT
+    if (hipError_t e = hipGetLastError()) return e;
+  }
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)(B * Hq)), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const uint64_t* bits, const uint16_t* scales, int64_t BH, int64_t tile_stride,
+                         int T, int tf, const int32_t* idx, int k, float* out, int64_t oss, int64_t ost,
+                         hipStream_t s) {
+  const int64_t nblk = BH * k * (T / 64);
+  if (nblk == 0) return hipSuccess;
+  dim3 grid((unsigned)nblk), block(64);
+#define KVR_GA(TV, TFV)                                                                            \
+  if (T == TV && tf == TFV) {                                                                      \
+    hipLaunchKernelGGL((gather_tiles_kernel<TV, TFV>), grid, block, 0, s, bits, scales, tile_stride, \
+                       idx, k, out, oss, ost);                                                     \
+    return hipGetLastError();                                                                      \
+  }
+  KVR_GA(64, KVR_HADAMARD)
+  KVR_GA(64, KVR_DCT)
+  KVR_GA(64, KVR_NONE)
+  KVR_GA(128, KVR_HADAMARD)
+  KVR_GA(128, KVR_DCT)
+  KVR_GA(128, KVR_NONE)
+#undef KVR_GA
+  return hipErrorInvalidValue;
+}
+
+}  // namespace kvr

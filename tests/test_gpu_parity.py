@@ -236,15 +236,23 @@ ATTN_CASES = [
     (2, 16, 2, 64, 64, 4, 0, 64, O.HADAMARD, "bf16", "fp16"),
     (2, 12, 4, 0, 64, 6, 4, 64, O.HADAMARD, "fp16", "fp16"),
     (1, 64, 4, 40, 64, 6, 2, 128, O.DCT, "fp32", "fp16"),
+    (1, 32, 8, 256, 256, 80, 37, 64, O.HADAMARD, "bf16", "bf16"),
 ]
+
+
+@pytest.fixture(params=["mfma", "valu"])
+def ret_method(request, monkeypatch):
+    """Both arithmetic paths of the retrieved tiles (read by the library at every launch)."""
+    monkeypatch.setenv("KVR_RETRIEVE_METHOD", request.param)
+    return request.param
 
 
 @pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_w{}_k{}_T{}_tf{}_{}_{}".format(
     c[0], c[1], c[2], c[3], c[6], c[7], c[8], c[9], c[10]))
 @pytest.mark.parametrize("odt", ["fp32", "bf16"])
-def test_decode_attn(H, rng, case, odt):
+def test_decode_attn(H, rng, case, odt, ret_method):
     B, Hq, Hkv, wl, wcap, n_tiles, k, T, tf, qdt, wdt = case
-    say(f"[decode_attn] {case} out={odt}")
+    say(f"[decode_attn] {case} out={odt} retrieve={ret_method}")
     S = B * Hkv
     q = torch.from_numpy(rng.standard_normal((B, Hq, 128)).astype(np.float32)).to(DEV, TDT[qdt])
     wk = torch.from_numpy(kv_like(rng, (B, Hkv, wcap, 128))).to(DEV, TDT[wdt])
@@ -276,8 +284,8 @@ def test_decode_attn_window_token_major_strides(H, rng):
     check_out(out, ref, "token-major window")
 
 
-def test_decode_attn_peaked_softmax(H, rng):
-    say("[decode_attn/peaked] one dominant window key and one dominant retrieved tile")
+def test_decode_attn_peaked_softmax(H, rng, ret_method):
+    say(f"[decode_attn/peaked] one dominant window key and one dominant retrieved tile ({ret_method})")
     B, Hq, Hkv, W, T = 1, 8, 2, 64, 64
     qn = rng.standard_normal((B, Hq, 128)).astype(np.float32)
     wkn = 0.1 * rng.standard_normal((B, Hkv, W, 128)).astype(np.float32)
@@ -298,8 +306,8 @@ def test_decode_attn_peaked_softmax(H, rng):
 # ----------------------------------------------------------------------------- full step
 
 @pytest.mark.parametrize("tf,T,Hq,Hkv", [(O.HADAMARD, 64, 32, 8), (O.DCT, 128, 28, 4)])
-def test_decode_step_matches_oracle_pipeline(H, rng, tf, T, Hq, Hkv):
-    say(f"[decode_step] tf={tf} T={T} Hq={Hq} Hkv={Hkv}")
+def test_decode_step_matches_oracle_pipeline(H, rng, tf, T, Hq, Hkv, ret_method):
+    say(f"[decode_step] tf={tf} T={T} Hq={Hq} Hkv={Hkv} retrieve={ret_method}")
     B, W, n_tok, k = 2, 256, 40 * T, 6
     K = torch.from_numpy(kv_like(rng, (B, Hkv, n_tok, 128))).to(DEV, torch.bfloat16)
     V = torch.from_numpy(rng.standard_normal((B, Hkv, n_tok, 128)).astype(np.float32)).to(DEV, torch.bfloat16)
