@@ -187,7 +187,7 @@ def decode_attn(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, idx, T, 
     wk, wv, wdt, wl, sb, sh, st = _window_args(win_k, win_v, win_len)
     need = lib().kvr_decode_attn_workspace(B, Hq, Hkv, wl, k, T)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=q.device)
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)
     out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
     tile_stride = kbits.shape[1] if kbits is not None else 1
     rc = lib().kvr_decode_attn(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, sb, sh, st,
@@ -199,9 +199,9 @@ def decode_attn(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, idx, T, 
 
 
 def decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T, device):
-    """Zero-filled workspace (its counters must start at zero; the kernels leave them zero)."""
+    """Workspace for decode_step (scores, indices, partial records; no initial contents needed)."""
     need = lib().kvr_decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T)
-    return torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
+    return torch.empty(max(need, 256), dtype=torch.uint8, device=device)
 
 
 def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles, T, transform, k,
