@@ -26,8 +26,10 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
                          const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
                          const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
                          const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
-                         float* scores, int32_t* idx, float* rec, void* out, int ot, hipStream_t s);
+                         float* scores, uint64_t* cand, int32_t* idx, float* rec, void* out, int ot,
+                         hipStream_t s);
 size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k);
+size_t cand_bytes(int64_t B, int Hkv, int64_t n_tiles, int k, int T);
 hipError_t launch_gather(const uint64_t* bits, const uint16_t* scales, int64_t BH,
                          int64_t tile_stride, int T, int tf, const int32_t* idx, int k, float* out,
                          int64_t oss, int64_t ost, hipStream_t s);
@@ -104,15 +106,18 @@ int check_store(const uint64_t* kb, const uint64_t* vb, const uint16_t* ks, cons
 }
 
 struct StepLayout {
-  size_t scores, idx, rec, total;
+  size_t scores, cand, idx, rec, total;
 };
 
-// Workspace: [scores | idx | partial records]; plain scratch, no state between calls.
-StepLayout step_layout(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles, int k) {
+// Workspace: [scores | candidate lists | idx | partial records]; plain scratch, no state
+// between calls.
+StepLayout step_layout(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles, int k, int T) {
   StepLayout L{};
   size_t off = 0;
   L.scores = off;
   off += round_up((size_t)(B * Hkv) * (size_t)(n_tiles > 0 ? n_tiles : 0) * sizeof(float));
+  L.cand = off;
+  off += round_up(kvr::cand_bytes(B, Hkv, n_tiles, k, T));
   L.idx = off;
   off += round_up((size_t)(B * Hkv) * (size_t)(k > 0 ? k : 0) * sizeof(int32_t));
   L.rec = off;
@@ -204,9 +209,8 @@ int kvr_topk_tiles(const float* scores, int64_t BH, int64_t n_tiles, int64_t sco
 }
 
 size_t kvr_decode_attn_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T) {
-  (void)T;
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv) return 0;
-  return step_layout(B, Hq, Hkv, win_len, 0, k).total;
+  return step_layout(B, Hq, Hkv, win_len, 0, k, T).total;
 }
 
 static int attn_checks(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
@@ -226,6 +230,7 @@ static int attn_checks(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, i
   if (k > 0)
     if (int r = check_store(kbits, vbits, kscale, vscale, tile_stride)) return r;
   if (B > 0 && (!q || !out)) return fail(KVR_ERR_INVALID, "q and out must be non-NULL");
+  if (B > 0 && !aligned(q, 16)) return fail(KVR_ERR_ALIGN, "q must be 16-byte aligned");
   if (B > 0 && !aligned(out, 8)) return fail(KVR_ERR_ALIGN, "out must be 8-byte aligned");
   return KVR_OK;
 }
@@ -243,7 +248,7 @@ int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
     return r;
   if (k > 0 && !idx) return fail(KVR_ERR_INVALID, "idx must be non-NULL when k > 0");
   if (B == 0) return KVR_OK;
-  const StepLayout L = step_layout(B, Hq, Hkv, win_len, 0, k);
+  const StepLayout L = step_layout(B, Hq, Hkv, win_len, 0, k, T);
   if (!workspace || ws_bytes < L.total)
     return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", L.total,
                 workspace ? ws_bytes : (size_t)0);
@@ -252,16 +257,16 @@ int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
   return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
                                        win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
                                        kscale, vscale, 0, tile_stride, T, transform, nullptr, nullptr,
-                                       k, false, nullptr, const_cast<int32_t*>(idx),
+                                       k, false, nullptr, nullptr, const_cast<int32_t*>(idx),
                                        (float*)(ws + L.rec), out, out_dtype, (hipStream_t)stream),
                     "kvr_decode_attn");
 }
 
 size_t kvr_decode_step_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles,
                                  int k, int T) {
-  (void)T;
-  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || n_tiles < 0) return 0;
-  return step_layout(B, Hq, Hkv, win_len, n_tiles, k).total;
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || n_tiles < 0 || (T != 64 && T != 128)) return 0;
+  if (n_tiles == 0) k = 0;
+  return step_layout(B, Hq, Hkv, win_len, k > 0 ? n_tiles : 0, k, T).total;
 }
 
 int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
@@ -284,7 +289,7 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
     return fail(KVR_ERR_INVALID, "excl_lo and excl_hi must both be given or both NULL");
   if (B == 0) return KVR_OK;
   const int64_t nt = (k > 0) ? n_tiles : 0;
-  const StepLayout L = step_layout(B, Hq, Hkv, win_len, nt, k);
+  const StepLayout L = step_layout(B, Hq, Hkv, win_len, nt, k, T);
   if (!workspace || ws_bytes < L.total)
     return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", L.total,
                 workspace ? ws_bytes : (size_t)0);
@@ -294,7 +299,8 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
   return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
                                        win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
                                        kscale, vscale, n_tiles, tile_stride, T, transform, excl_lo,
-                                       excl_hi, k, true, (float*)(ws + L.scores), idx,
+                                       excl_hi, k, true, (float*)(ws + L.scores),
+                                       (uint64_t*)(ws + L.cand), idx,
                                        (float*)(ws + L.rec), out, out_dtype, (hipStream_t)stream),
                     "kvr_decode_step");
 }

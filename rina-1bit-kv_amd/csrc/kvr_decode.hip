@@ -5,14 +5,17 @@
 // One decode step (kvr_decode_step) is three launches and no block ever waits for
 // another block inside a launch (an agent-scope fence costs an L2 write-back on
 // gfx950, so cross-block hand-offs inside a kernel are avoided):
-//   score   : one item per (segment, 64 tiles); the block rotates the segment's
-//             GQA-mean query itself and writes fp32 scores.  (segment = sequence x
-//             KV head)
-//   attend  : window items (128 window tokens of one segment, MFMA) interleaved with
-//             retrieved items (4 selected tiles of one segment, one per wave, VALU
-//             bit-unpack); a retrieved item first selects its segment's top-k from
-//             the scores (every item of the segment computes the same selection).
-//             Both write partial softmax records.
+//   score   : one item per (segment, 64 tiles) (segment = sequence x KV head); the
+//             block loads its tile words first, rotates the segment's GQA-mean query
+//             meanwhile, writes fp32 scores and (k <= 64) its tiles sorted by
+//             (score desc, tile asc) as a candidate list.
+//   attend  : per segment, retrieved items (8 selected tiles, two per wave, MFMA on
+//             +-1 operands) followed by window items (up to 512 window tokens; K
+//             into registers, V rows straight into LDS by direct loads, MFMA,
+//             software-pipelined over 32-token chunks).  A retrieved item first
+//             selects the segment's top-k by merging the candidate lists (every
+//             item of the segment computes the same selection).  Both write
+//             partial softmax records.
 //   merge   : log-sum-exp merge of a segment's records, inverse rotation of the
 //             retrieved part, output.
 //
@@ -34,10 +37,22 @@
 namespace kvr {
 
 constexpr int NT = 256;           // threads per block (4 waves) for every decode role
-constexpr int SCORE_TILES = 64;   // tiles per score item (16 groups x 4)
-constexpr int WIN_SPAN = 512;     // window tokens per window item (4 waves x 4 chunks of 32)
-constexpr int WIN_CHUNK = 32;
-constexpr int VROW = D + 8;       // bf16 elements per staged V row (16 B pad)
+// Build-time tuning (defaults are the measured best on MI355X): waves per SIMD the
+// attend kernel is compiled for (sets its VGPR budget), the number of window items
+// below which window spans stay at one chunk per wave, and the selected tiles per
+// retrieved item.
+#ifndef KVR_ATTEND_WAVES
+#define KVR_ATTEND_WAVES 3
+#endif
+#ifndef KVR_WIN_MIN_ITEMS
+#define KVR_WIN_MIN_ITEMS 256
+#endif
+#ifndef KVR_RET_TILES
+#define KVR_RET_TILES 8  // selected tiles per retrieved item (a multiple of 4: one per wave per round)
+#endif
+
+constexpr int WIN_CHUNK = 32;     // window tokens per wave per step
+constexpr int WIN_UNIT = 4 * WIN_CHUNK;  // window items span a multiple of this
 constexpr int TOPK_MAX_K = 1024;
 constexpr float SCALE_LOG2 = 0.08838834764831845f * LOG2E;  // log2(e) / sqrt(128)
 
@@ -56,9 +71,11 @@ struct DecodeArgs {
   const int32_t* excl_hi;
   int k;
   float* scores;      // [BH][n_tiles]
+  uint64_t* cand;     // [BH][n_chunks][64] per-item candidates, sorted (k <= 64), or null
   int32_t* idx;       // [BH][k]
   float* rec;         // [BH][n_parts][g][2+D]
   int n_chunks, n_wparts, n_rparts;
+  int64_t win_span;   // window tokens per window item
   int do_select;      // retrieved items select their tiles from scores (else read idx)
   int ret_method;     // retrieved tiles: 0 = MFMA on unpacked +-1 operands, 1 = VALU nibble tables
   void* out;          // [B][Hq][D]
@@ -71,6 +88,10 @@ __device__ __forceinline__ float q_elem(const DecodeArgs& a, int64_t i) {
   if (a.q_dtype == KVR_FP16) return load_as_f32<KVR_FP16>(a.q, i);
   return load_as_f32<KVR_FP32>(a.q, i);
 }
+
+// Materialise a loaded value here: keeps the compiler from sinking a load into the
+// branch that uses it (which would serialise loads meant to be in flight together).
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
 // LDS in-order completion within one wave (no block barrier).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -90,14 +111,42 @@ __device__ __forceinline__ void unrotate_pair(float& v0, float& v1, int lane, in
 
 // Rotated GQA-mean query of one segment into qs[128] (one wave; lane = channels
 // 2*lane, 2*lane+1).  fp32 sum in head order, one correctly rounded division.
+// Two consecutive query elements (even offset) by one 4- or 8-byte load.
+__device__ __forceinline__ void q_pair(const DecodeArgs& a, int64_t off, float& v0, float& v1) {
+  if (a.q_dtype == KVR_FP32) {
+    const float2 u = *(const float2*)((const float*)a.q + off);
+    v0 = u.x;
+    v1 = u.y;
+  } else {
+    const uint32_t r = *(const uint32_t*)((const uint16_t*)a.q + off);
+    const uint16_t lo = (uint16_t)(r & 0xffffu), hi = (uint16_t)(r >> 16);
+    v0 = (a.q_dtype == KVR_BF16) ? bf16_to_f32(lo) : f16_to_f32(lo);
+    v1 = (a.q_dtype == KVR_BF16) ? bf16_to_f32(hi) : f16_to_f32(hi);
+  }
+}
+
+// Rotated GQA-mean query of a segment into qs[128] (one wave; lane = channel pair).
+// All g heads are loaded first (clamped, branch-free) so the loads are in flight together,
+// then summed in head order.
 __device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs, int lane) {
   const int64_t b = seg / a.Hkv;
   const int h = (int)(seg - b * a.Hkv);
-  const int64_t q0 = (b * a.Hq + (int64_t)h * a.g) * D;
-  float m0 = q_elem(a, q0 + 2 * lane), m1 = q_elem(a, q0 + 2 * lane + 1);
-  for (int i = 1; i < a.g; ++i) {
-    m0 = m0 + q_elem(a, q0 + (int64_t)i * D + 2 * lane);
-    m1 = m1 + q_elem(a, q0 + (int64_t)i * D + 2 * lane + 1);
+  const int64_t q0 = (b * a.Hq + (int64_t)h * a.g) * D + 2 * lane;
+  float v0[16], v1[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) q_pair(a, q0 + (int64_t)(i < a.g ? i : 0) * D, v0[i], v1[i]);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    pin(v0[i]);
+    pin(v1[i]);
+  }
+  float m0 = v0[0], m1 = v1[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    if (i < a.g) {
+      m0 = m0 + v0[i];
+      m1 = m1 + v1[i];
+    }
   }
   m0 = __fdiv_rn(m0, (float)a.g);
   m1 = __fdiv_rn(m1, (float)a.g);
@@ -105,6 +154,15 @@ __device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs
   qs[2 * lane] = m0;
   qs[2 * lane + 1] = m1;
 }
+
+// Selection candidate (score_key << 32) | (0xffffffff - tile): a larger value is a
+// better candidate in the (score desc, tile asc) order; 0 pads below every real key.
+__device__ __forceinline__ uint64_t pack_cand(uint32_t key, uint32_t tile) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - tile);
+}
+__device__ __forceinline__ uint32_t cand_tile(uint64_t v) { return 0xffffffffu - (uint32_t)v; }
+
+__device__ const int32_t g_zero_i32 = 0;  // exclusion bound when no range is given
 
 // ------------------------------------------------------------------ scoring
 
@@ -129,16 +187,50 @@ __device__ __forceinline__ float tree16(float p) {
   return p;
 }
 
-// Score tiles [t0, t1) of one segment.  16 lanes per tile, lane li owns channels
-// 8li..8li+7: per-lane sequential fp32 sum of fl(q*c), then the 16-lane tree.
-template <int T, int METHOD>
-__device__ void score_tiles_block(const float* qs, const uint64_t* kbits, int64_t seg, int64_t n_tiles,
-                                  int64_t tile_stride, int64_t t0, int64_t t1, int32_t lo, int32_t hi,
-                                  float* scores) {
+// Score items: 16 lanes per tile, lane li owns channels 8li..8li+7; each 16-lane group
+// scores TPG tiles (64 words in flight per lane for either T), so an item covers
+// 16*TPG tiles.  The words are loaded before the query is ready (one HBM round trip
+// per item, overlapped with the query prologue).
+template <int T>
+struct ScoreWords {
+  static constexpr int W = T / 64;
+  static constexpr int TPG = 4 / W;
+  uint64_t w[TPG][8 * W];
+};
+
+constexpr int score_tiles_per_item(int T) { return 16 * (4 / (T / 64)); }
+
+template <int T>
+__device__ __forceinline__ void score_load(const uint64_t* kbits, int64_t seg, int64_t tile_stride,
+                                           int64_t t0, int64_t t1, ScoreWords<T>& sw) {
   constexpr int W = T / 64;
-  const int tid = threadIdx.x;
-  const int grp = tid >> 4;
-  const int li = tid & 15;
+  constexpr int TPG = ScoreWords<T>::TPG;
+  const int grp = threadIdx.x >> 4;
+  const int li = threadIdx.x & 15;
+  const uint64_t* segbits = kbits + seg * tile_stride * (int64_t)(D * W);
+#pragma unroll
+  for (int i = 0; i < TPG; ++i) {
+    int64_t tile = t0 + grp + 16 * i;
+    tile = tile < t1 ? tile : t0;  // t0 < t1 <= tile_stride: always a stored tile
+    const ulonglong2* wp = (const ulonglong2*)(segbits + tile * (D * W) + 8 * li * W);
+#pragma unroll
+    for (int j = 0; j < 4 * W; ++j) {
+      const ulonglong2 v = wp[j];
+      sw.w[i][2 * j] = v.x;
+      sw.w[i][2 * j + 1] = v.y;
+    }
+  }
+}
+
+// Per-lane sequential fp32 sum of fl(q*c) over its 8 channels, then the 16-lane tree.
+template <int T, int METHOD>
+__device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<T>& sw, int64_t seg,
+                                              int64_t n_tiles, int64_t t0, int64_t t1, int32_t lo,
+                                              int32_t hi, float* scores, uint64_t* lc = nullptr) {
+  constexpr int W = T / 64;
+  constexpr int TPG = ScoreWords<T>::TPG;
+  const int grp = threadIdx.x >> 4;
+  const int li = threadIdx.x & 15;
   float q[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) q[k] = qs[8 * li + k];
@@ -147,23 +239,16 @@ __device__ void score_tiles_block(const float* qs, const uint64_t* kbits, int64_
   for (int k = 1; k < 8; ++k) qq = qq + q[k] * q[k];
   qq = tree16(qq);
   const float qn = sqrt_rn(qq) + EPS;
-  const uint64_t* segbits = kbits + seg * tile_stride * (int64_t)(D * W);
-  for (int64_t tile = t0 + grp; tile < t1; tile += 16) {
-    const uint64_t* wp = segbits + tile * (D * W) + 8 * li * W;
-    uint64_t wd[8 * W];
 #pragma unroll
-    for (int i = 0; i < 4 * W; ++i) {
-      ulonglong2 v = ((const ulonglong2*)wp)[i];
-      wd[2 * i] = v.x;
-      wd[2 * i + 1] = v.y;
-    }
+  for (int i = 0; i < TPG; ++i) {
+    const int64_t tile = t0 + grp + 16 * i;
     float dot = 0.f;
     int cc = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       int pc = 0;
 #pragma unroll
-      for (int w = 0; w < W; ++w) pc += count_bits<METHOD>(wd[k * W + w]);
+      for (int w = 0; w < W; ++w) pc += count_bits<METHOD>(sw.w[i][k * W + w]);
       const int c = 2 * pc - T;
       cc += c * c;
       const float prod = q[k] * (float)c;
@@ -174,12 +259,13 @@ __device__ void score_tiles_block(const float* qs, const uint64_t* kbits, int64_
     cc += __shfl_xor(cc, 4, 64);
     cc += __shfl_xor(cc, 2, 64);
     cc += __shfl_xor(cc, 1, 64);
-    if (li == 0) {
+    if (li == 0 && tile < t1) {
       const float cn = sqrt_rn((float)cc) + EPS;
       float sc = __fdiv_rn(dot, qn * cn);
       if (sc != sc) sc = -__builtin_inff();
       if (tile >= lo && tile < hi) sc = -__builtin_inff();
       scores[seg * n_tiles + tile] = sc;
+      if (lc) lc[grp + 16 * i] = pack_cand(score_key(sc), (uint32_t)tile);
     }
   }
 }
@@ -192,42 +278,189 @@ struct TopkSmem {
   int32_t seli[TOPK_MAX_K];
 };
 
-// Writes the k winners (key, index) into sm.selk / sm.seli in index order of the
-// two classes (keys > tau first, then the first kk keys == tau), then rank-sorts
-// them by (key desc, index asc) into out[0..k).
-__device__ void topk_rank_out(int k, int32_t* out, TopkSmem& sm, int lane) {
-  wave_lds_sync();
-  for (int ai = lane; ai < k; ai += 64) {
-    const uint32_t ka = sm.selk[ai];
-    const int32_t ia = sm.seli[ai];
-    int rank = 0;
-    for (int bi = 0; bi < k; ++bi) {
-      const uint32_t kb = sm.selk[bi];
-      const int32_t ib = sm.seli[bi];
-      rank += (kb > ka) || (kb == ka && ib < ia);
-    }
-    out[rank] = ia;
+// One compare-exchange stage of a 64-lane bitonic sort of (key, idx) pairs into the
+// order key descending, idx ascending: block size S, partner lane ^ J.
+template <int S, int J>
+__device__ __forceinline__ void bitonic_step(uint32_t& key, int32_t& idx, int lane) {
+  const uint32_t ok = xor_lane_u<J>(key);
+  const int32_t oi = (int32_t)xor_lane_u<J>((uint32_t)idx);
+  const bool lower = (lane & J) == 0;
+  const bool asc = (lane & S) == 0;
+  const bool mine_first = (key > ok) || (key == ok && idx < oi);
+  if (mine_first != (lower == asc)) {
+    key = ok;
+    idx = oi;
   }
 }
 
+// Writes the k winners (key, index) into sm.selk / sm.seli in index order of the
+// two classes (keys > tau first, then the first kk keys == tau), then orders them by
+// (key desc, index asc) into out[0..k): a bitonic sort across the wave for k <= 64
+// (padding sorts last), else each lane ranks one candidate per round of 64 against
+// every candidate broadcast by readlane.
+__device__ __forceinline__ void topk_rank_out(int k, int32_t* out, TopkSmem& sm, int lane) {
+  wave_lds_sync();
+  if (k <= 64) {
+    uint32_t key = (lane < k) ? sm.selk[lane] : 0u;
+    int32_t idx = (lane < k) ? sm.seli[lane] : 0x7fffffff;
+    bitonic_step<2, 1>(key, idx, lane);
+    bitonic_step<4, 2>(key, idx, lane);
+    bitonic_step<4, 1>(key, idx, lane);
+    bitonic_step<8, 4>(key, idx, lane);
+    bitonic_step<8, 2>(key, idx, lane);
+    bitonic_step<8, 1>(key, idx, lane);
+    bitonic_step<16, 8>(key, idx, lane);
+    bitonic_step<16, 4>(key, idx, lane);
+    bitonic_step<16, 2>(key, idx, lane);
+    bitonic_step<16, 1>(key, idx, lane);
+    bitonic_step<32, 16>(key, idx, lane);
+    bitonic_step<32, 8>(key, idx, lane);
+    bitonic_step<32, 4>(key, idx, lane);
+    bitonic_step<32, 2>(key, idx, lane);
+    bitonic_step<32, 1>(key, idx, lane);
+    bitonic_step<64, 32>(key, idx, lane);
+    bitonic_step<64, 16>(key, idx, lane);
+    bitonic_step<64, 8>(key, idx, lane);
+    bitonic_step<64, 4>(key, idx, lane);
+    bitonic_step<64, 2>(key, idx, lane);
+    bitonic_step<64, 1>(key, idx, lane);
+    if (lane < k) out[lane] = idx;
+    return;
+  }
+  for (int a0 = 0; a0 < k; a0 += 64) {
+    const bool act = a0 + lane < k;
+    const uint32_t ka = act ? sm.selk[a0 + lane] : 0u;
+    const int32_t ia = act ? sm.seli[a0 + lane] : 0;
+    int rank = 0;
+    for (int b0 = 0; b0 < k; b0 += 64) {
+      const bool bv = b0 + lane < k;
+      const uint32_t kbv = bv ? sm.selk[b0 + lane] : 0u;
+      const int32_t ibv = bv ? sm.seli[b0 + lane] : 0;
+      const int nb = (k - b0 < 64) ? k - b0 : 64;
+      for (int j = 0; j < nb; ++j) {
+        const uint32_t kb = (uint32_t)__builtin_amdgcn_readlane((int)kbv, j);
+        const int32_t ib = __builtin_amdgcn_readlane(ibv, j);
+        rank += (kb > ka) || (kb == ka && ib < ia);
+      }
+    }
+    if (act) out[rank] = ia;
+  }
+}
+
+// ---- two-level selection for k <= 64: every score item sorts its (up to 64) tiles,
+// the retrieved items merge the per-item lists.  A candidate is packed as
+// (score_key << 32) | (0xffffffff - tile), so a larger value is a better candidate in
+// exactly the (score desc, tile asc) order; 0 pads (below every real key).
+
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v) {
+  const uint32_t lo = xor_lane_u<J>((uint32_t)v), hi = xor_lane_u<J>((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Compare-exchange stage of a 64-lane bitonic network sorting descending: block size S
+// (S = 128: the whole wave is one descending block), partner lane ^ J.
+template <int S, int J>
+__device__ __forceinline__ void bitonic64(uint64_t& v, int lane) {
+  const uint64_t o = xor_lane_u64<J>(v);
+  const bool lower = (lane & J) == 0;
+  const bool desc = (S >= 128) || ((lane & S) == 0);
+  const bool keep_max = (lower == desc);
+  v = keep_max ? (v > o ? v : o) : (v > o ? o : v);
+}
+
+// Full descending sort of one value per lane.
+__device__ __forceinline__ void sort64_desc(uint64_t& v, int lane) {
+  bitonic64<2, 1>(v, lane);
+  bitonic64<4, 2>(v, lane);
+  bitonic64<4, 1>(v, lane);
+  bitonic64<8, 4>(v, lane);
+  bitonic64<8, 2>(v, lane);
+  bitonic64<8, 1>(v, lane);
+  bitonic64<16, 8>(v, lane);
+  bitonic64<16, 4>(v, lane);
+  bitonic64<16, 2>(v, lane);
+  bitonic64<16, 1>(v, lane);
+  bitonic64<32, 16>(v, lane);
+  bitonic64<32, 8>(v, lane);
+  bitonic64<32, 4>(v, lane);
+  bitonic64<32, 2>(v, lane);
+  bitonic64<32, 1>(v, lane);
+  bitonic64<128, 32>(v, lane);
+  bitonic64<128, 16>(v, lane);
+  bitonic64<128, 8>(v, lane);
+  bitonic64<128, 4>(v, lane);
+  bitonic64<128, 2>(v, lane);
+  bitonic64<128, 1>(v, lane);
+}
+
+// Top 64 of two descending lists: lane l holds a[l] and b[63 - l]; max(a[l], b[63-l])
+// is bitonic and holds the 64 largest, which six stages sort descending.
+__device__ __forceinline__ uint64_t merge_top64(uint64_t a, uint64_t b_rev, int lane) {
+  uint64_t v = a > b_rev ? a : b_rev;
+  bitonic64<128, 32>(v, lane);
+  bitonic64<128, 16>(v, lane);
+  bitonic64<128, 8>(v, lane);
+  bitonic64<128, 4>(v, lane);
+  bitonic64<128, 2>(v, lane);
+  bitonic64<128, 1>(v, lane);
+  return v;
+}
+
+// sel[0..k) from the n_lists descending candidate lists of a segment (k <= 64): all
+// lists are loaded first (list i reversed for lanes, clamped), then merged in order.
+__device__ __forceinline__ void select_from_cands(const uint64_t* lists, int n_lists, int k, int32_t* sel,
+                                                  int lane) {
+  constexpr int BATCH = 8;
+  uint64_t acc = lists[lane];
+  for (int c0 = 1; c0 < n_lists; c0 += BATCH) {
+    uint64_t b[BATCH];
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      const int c = (c0 + i < n_lists) ? c0 + i : n_lists - 1;
+      b[i] = lists[(int64_t)c * 64 + (63 - lane)];
+    }
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i)
+      if (c0 + i < n_lists) acc = merge_top64(acc, b[i], lane);
+  }
+  if (lane < k) sel[lane] = (int32_t)cand_tile(acc);
+}
+
 // Register-resident select for n <= 64*KPL: bitwise (MSB-first) search of tau, the
-// largest key with #{key >= tau} >= k, by wave ballots; no LDS atomics.
+// largest key with #{key >= tau} >= k, from per-lane counts summed across the wave;
+// no LDS atomics.
 template <int KPL>
-__device__ void topk_wave_regs(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
+__device__ __forceinline__ void topk_wave_regs(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
   uint32_t key[KPL];
+  float vals[KPL];
 #pragma unroll
   for (int r = 0; r < KPL; ++r) {
     const int64_t i = (int64_t)r * 64 + lane;
-    key[r] = (i < n) ? score_key(row[i]) : 0u;  // padding sorts below every score (even -inf)
+    vals[r] = row[i < n ? i : n - 1];  // clamped: every lane loads, all loads in flight
   }
+#pragma unroll
+  for (int r = 0; r < KPL; ++r) pin(vals[r]);
+#pragma unroll
+  for (int r = 0; r < KPL; ++r) {
+    const int64_t i = (int64_t)r * 64 + lane;
+    key[r] = (i < n) ? score_key(vals[r]) : 0u;  // padding sorts below every score (even -inf)
+  }
+  // MSB-first search; the count of keys >= cand is summed per lane, then across the
+  // wave by DPP.  A count of exactly k ends the search: the keys >= tau are then the
+  // answer (the tie classes below handle it unchanged).
   uint32_t tau = 0;
 #pragma unroll 1
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = tau | (1u << bit);
-    int cnt = 0;
+    float c = 0.f;
 #pragma unroll
-    for (int r = 0; r < KPL; ++r) cnt += __popcll(__ballot(key[r] >= cand));
-    if (cnt >= k) tau = cand;
+    for (int r = 0; r < KPL; ++r) c += (key[r] >= cand) ? 1.f : 0.f;
+    const int cnt = __builtin_amdgcn_readfirstlane((int)wave_sum(c));
+    if (cnt >= k) {
+      tau = cand;
+      if (cnt == k) break;
+    }
   }
   int n_gt = 0;
 #pragma unroll
@@ -259,7 +492,7 @@ __device__ void topk_wave_regs(const float* row, int64_t n, int k, int32_t* out,
 }
 
 // Any n: 4 x 8-bit radix passes with an LDS histogram, keys re-read from row.
-__device__ void topk_wave_hist(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
+__device__ __forceinline__ void topk_wave_hist(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
   uint32_t prefix = 0, pmask = 0, kk = (uint32_t)k;
 #pragma unroll 1
   for (int shift = 24; shift >= 0; shift -= 8) {
@@ -337,11 +570,20 @@ __device__ void topk_wave_hist(const float* row, int64_t n, int k, int32_t* out,
 
 // idx[0..k) = indices of the k largest scores of row[0..n), score descending then
 // index ascending (NaN counts as -inf).
-__device__ void topk_wave(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
+__device__ __forceinline__ void topk_wave(const float* row, int64_t n, int k, int32_t* out, TopkSmem& sm, int lane) {
   if (n <= 512) topk_wave_regs<8>(row, n, k, out, sm, lane);
   else if (n <= 1024) topk_wave_regs<16>(row, n, k, out, sm, lane);
   else if (n <= 2048) topk_wave_regs<32>(row, n, k, out, sm, lane);
   else topk_wave_hist(row, n, k, out, sm, lane);
+}
+
+// The k selected tiles of a segment into sel[0..k): from the score items' sorted
+// candidate lists when they were written (k <= 64), else by the wave select over the
+// segment's scores.
+__device__ __forceinline__ void select_tiles(const DecodeArgs& a, int64_t seg, int k, int32_t* sel,
+                                             TopkSmem& tk, int lane) {
+  if (a.cand) select_from_cands(a.cand + seg * a.n_chunks * (int64_t)64, a.n_chunks, k, sel, lane);
+  else topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sel, tk, lane);
 }
 
 // ------------------------------------------------------------------ MFMA helpers
@@ -377,13 +619,62 @@ __device__ __forceinline__ void split16(float x, uint32_t* part) {
 
 __device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) { return lo16 | (hi16 << 16); }
 
-// Combine per-wave softmax partials of one block into a record.  Each wave
-// holds (m_w, l_w) per head column and o contributions; ost is LDS [16][128].
+// Combine the 4 waves' softmax partials of one block into a record [m[g] | l[g] |
+// o[g][128]].  Each wave leaves (m, l) per head column and its unscaled o in its own
+// region ow[w][d*16 + n]; after one barrier every thread scales and sums the 4 waves'
+// values of its (head, dim) elements in wave order.
 struct CombineSmem {
   float cm[4][16];
   float cl[4][16];
 };
+constexpr int OW_WAVE = 16 * D;  // floats of one wave's partial o
 
+template <typename DimOf>
+__device__ __forceinline__ void combine_record(const f32x4 (&oacc)[8], float m_run, float l_run, float* ow,
+                                               CombineSmem& cs, int g, float* R, DimOf dim_of) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  if (kg == 0) {
+    cs.cm[w][n] = m_run;
+    cs.cl[w][n] = l_run;
+  }
+  if (n < g) {
+    float* o = ow + w * OW_WAVE;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[dim_of(i, r, kg) * 16 + n] = oacc[i][r];
+  }
+  __syncthreads();
+  if (tid < g) {
+    float mh = -__builtin_inff();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) mh = fmaxf(mh, cs.cm[v][tid]);
+    const float muh = (mh == -__builtin_inff()) ? 0.f : mh;
+    float lt = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) lt += cs.cl[v][tid] * exp2f(cs.cm[v][tid] - muh);
+    R[tid] = mh;
+    R[g + tid] = lt;
+  }
+  for (int e = tid; e < g * D; e += NT) {
+    const int hn = e >> 7, d = e & (D - 1);
+    float mh = -__builtin_inff();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) mh = fmaxf(mh, cs.cm[v][hn]);
+    const float muh = (mh == -__builtin_inff()) ? 0.f : mh;
+    float acc = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc += ow[v * OW_WAVE + d * 16 + hn] * exp2f(cs.cm[v][hn] - muh);
+    R[2 * g + e] = acc;
+  }
+}
+
+// Record stats from the per-wave (m, l) already in cs (the VALU retrieved role, which
+// accumulates o in LDS itself).
 __device__ void write_record_stats(const CombineSmem& cs, float* R, int g, int tid) {
   if (tid < g) {
     float mh = -__builtin_inff();
@@ -402,17 +693,45 @@ __device__ void write_record_stats(const CombineSmem& cs, float* R, int g, int t
 
 struct WindowSmem {
   union {
-    uint16_t vstage[4][WIN_CHUNK * VROW];  // per-wave V staging
-    float ost[16 * D];                      // combine buffer (after the main loop)
+    uint16_t vstage[4][WIN_CHUNK * D];  // per-wave V rows, written by direct LDS loads
+    float ow[4 * OW_WAVE];              // per-wave partial o (each over its own V rows)
   };
   CombineSmem cs;
 };
+static_assert(sizeof(uint16_t) * WIN_CHUNK * D == sizeof(float) * OW_WAVE, "ow[w] must overlay vstage[w]");
+
+// Eight consecutive query elements (16-byte aligned) as floats.
+__device__ __forceinline__ void q_load8(const DecodeArgs& a, int64_t off, float* x) {
+  if (a.q_dtype == KVR_FP32) {
+    const float4 u = *(const float4*)((const float*)a.q + off);
+    const float4 v = *(const float4*)((const float*)a.q + off + 4);
+    x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+    x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+  } else {
+    const u32x4 r = *(const u32x4*)((const uint16_t*)a.q + off);
+    const bool bf = a.q_dtype == KVR_BF16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = (uint16_t)(r[i] & 0xffffu), hi = (uint16_t)(r[i] >> 16);
+      x[2 * i] = bf ? bf16_to_f32(lo) : f16_to_f32(lo);
+      x[2 * i + 1] = bf ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+  }
+}
+
+// Wait for this wave's outstanding vector-memory loads (including direct LDS loads).
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0)
+
+typedef void __attribute__((address_space(3))) * lds_ptr_t;
 
 // S^T[16 tok x 16 heads] = K[16 x 32 dims] Q^T[32 x 16];  O^T[16 dims x 16 heads] +=
 // V^T[16 dims x 32 tok] P^T[32 tok x 16 heads].  Lane (n = lane & 15, kg = lane >> 4):
 // Q^T/P^T column n = head n; S^T rows 4kg..4kg+3 of a 16-token block are tokens
 // 16 tb + 4kg + r, which is the k-slot (kg, e = 4 tb + r) of the PV product, so the
 // probabilities feed the B operand in place.  Block i of O^T has row m <-> dim 8m+i.
+// K comes straight into registers in A-operand order; V rows go from HBM to the wave's
+// LDS rows by direct 16-byte LDS loads (lane l of load i: token 4i + l/16, dims
+// 8 (l%16) ..), both issued before the query is read.
 template <int WDT, int QS, int PS>
 __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
   const int tid = threadIdx.x;
@@ -424,17 +743,46 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
   const int64_t b = seg / a.Hkv;
   const int64_t h = seg - b * a.Hkv;
 
+  const uint16_t* kbase = a.wk + b * a.sb + h * a.sh;
+  const uint16_t* vbase = a.wv + b * a.sb + h * a.sh;
+  const int64_t win_len = a.win_len, st = a.st;
+  const int64_t t_begin = (int64_t)part * a.win_span;
+  const int64_t t_end = (t_begin + a.win_span < win_len) ? t_begin + a.win_span : win_len;
+  uint16_t* vs = sm.vstage[wv_id];
+
+  u32x4 ka[2][4];
+  auto issue_chunk = [&](int64_t c0) {
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      int64_t tok = c0 + 16 * tb + n;
+      tok = tok < win_len ? tok : win_len - 1;  // clamped rows are masked below
+      const uint16_t* kr = kbase + tok * st + 8 * kg;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) ka[tb][ks] = *(const u32x4*)(kr + 32 * ks);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int64_t tok = c0 + 4 * i + kg;
+      tok = tok < win_len ? tok : win_len - 1;
+      __builtin_amdgcn_global_load_lds((const void*)(vbase + tok * st + 8 * n), (lds_ptr_t)(vs + i * 4 * D),
+                                       16, 0, 0);
+    }
+  };
+  int64_t c0 = t_begin + (int64_t)wv_id * WIN_CHUNK;
+  if (c0 < t_end) issue_chunk(c0);
+
   u32x4 qb[QS][4];
   {
-    const int64_t qoff = (b * a.Hq + h * g + n) * D;
+    const int64_t qoff = (b * a.Hq + h * g + (n < g ? n : 0)) * D;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
+      float x[8];
+      q_load8(a, qoff + 32 * ks + 8 * kg, x);
       uint32_t pe[QS][8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = (n < g) ? q_elem(a, qoff + 32 * ks + 8 * kg + e) : 0.f;
         uint32_t p[QS];
-        split16<WDT, QS>(x, p);
+        split16<WDT, QS>(n < g ? x[e] : 0.f, p);
 #pragma unroll
         for (int sp = 0; sp < QS; ++sp) pe[sp][e] = p[sp];
       }
@@ -451,30 +799,10 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
   float m_run = -__builtin_inff();
   float l_run = 0.f;
 
-  const uint16_t* kbase = a.wk + b * a.sb + h * a.sh;
-  const uint16_t* vbase = a.wv + b * a.sb + h * a.sh;
-  const int64_t win_len = a.win_len, st = a.st;
-  const int64_t t_begin = (int64_t)part * WIN_SPAN;
-  const int64_t t_end = (t_begin + WIN_SPAN < win_len) ? t_begin + WIN_SPAN : win_len;
-  uint16_t* vs = sm.vstage[wv_id];
-
-  for (int64_t c0 = t_begin + (int64_t)wv_id * WIN_CHUNK; c0 < t_end; c0 += 4 * WIN_CHUNK) {
-    u32x4 ka[2][4];
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      int64_t tok = c0 + 16 * tb + n;
-      tok = tok < win_len ? tok : win_len - 1;
-      const uint16_t* kr = kbase + tok * st + 8 * kg;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) ka[tb][ks] = *(const u32x4*)(kr + 32 * ks);
-    }
-    u32x4 vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int64_t tok = c0 + 4 * i + kg;
-      tok = tok < win_len ? tok : win_len - 1;
-      vr[i] = *(const u32x4*)(vbase + tok * st + 8 * n);
-    }
+  // Chunk c: wait for its K (registers) and V rows (LDS), S = K Q^T, read the V rows
+  // into registers, then issue chunk c+1's loads, which fly during softmax and PV.
+  for (; c0 < t_end; c0 += 4 * WIN_CHUNK) {
+    wait_vm();
     f32x4 s[2];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
@@ -484,8 +812,16 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 #pragma unroll
         for (int sp = 0; sp < QS; ++sp) s[tb] = mfma16<WDT>(ka[tb][ks], qb[sp][ks], s[tb]);
     }
+    u32x4 rv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *(u32x4*)(vs + (4 * i + kg) * VROW + 8 * n) = vr[i];
+    for (int e = 0; e < 8; ++e) {
+      const int trow = 16 * (e >> 2) + 4 * kg + (e & 3);
+      rv[e] = *(const u32x4*)(vs + trow * D + 8 * n);
+    }
+    if (c0 + 4 * WIN_CHUNK < t_end) {
+      wave_lds_sync();  // this chunk's V rows are in registers before they are reloaded
+      issue_chunk(c0 + 4 * WIN_CHUNK);
+    }
 
     float l2[8];
     float cmax = -__builtin_inff();
@@ -528,13 +864,6 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
         pb[sp] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
                        pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
     }
-    wave_lds_sync();
-    u32x4 rv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int trow = 16 * (e >> 2) + 4 * kg + (e & 3);
-      rv[e] = *(const u32x4*)(vs + trow * VROW + 8 * n);
-    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
@@ -544,36 +873,33 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 #pragma unroll
       for (int sp = 0; sp < PS; ++sp) oacc[i] = mfma16<WDT>(av, pb[sp], oacc[i]);
     }
-    __builtin_amdgcn_wave_barrier();
   }
 
   l_run += xor16_f(l_run);
   l_run += xor32_f(l_run);
-  if (kg == 0) {
-    sm.cs.cm[wv_id][n] = m_run;
-    sm.cs.cl[wv_id][n] = l_run;
+  float* R = a.rec + (seg * (a.n_wparts + a.n_rparts) + part) * (int64_t)(g * (2 + D));
+  // oacc[i][r] of lane (n, kg) is dim 32 kg + 8 r + i
+  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, R,
+                 [](int i, int r, int kgv) { return 32 * kgv + 8 * r + i; });
+}
+
+// Query heads h0, h0 + step, ... (up to QH_MAX of them, the slots a wave rotates) of a
+// segment: channel pair 2 lane, 2 lane + 1; loads clamped to head 0 past g, all issued
+// before any is used.
+constexpr int QH_MAX = 6;  // ceil(16 / 3): heads per wave when 3 waves share 16 slots
+__device__ __forceinline__ void load_heads(const DecodeArgs& a, int64_t b, int64_t h, int h0, int step,
+                                           int lane, float* v0, float* v1) {
+  const int64_t base = (b * a.Hq + h * a.g) * D + 2 * lane;
+#pragma unroll
+  for (int j = 0; j < QH_MAX; ++j) {
+    const int hh = h0 + step * j;
+    q_pair(a, base + (int64_t)(hh < a.g ? hh : 0) * D, v0[j], v1[j]);
   }
-  __syncthreads();
-  float mx = -__builtin_inff();
 #pragma unroll
-  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm.cs.cm[w][n]);
-  const float fw = exp2f(m_run - ((mx == -__builtin_inff()) ? 0.f : mx));
-  for (int i = tid; i < 16 * D; i += NT) sm.ost[i] = 0.f;
-  __syncthreads();
-#pragma unroll 1
-  for (int w = 0; w < 4; ++w) {
-    if (wv_id == w && n < g) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sm.ost[n * D + 32 * kg + 8 * r + i] += oacc[i][r] * fw;
-    }
-    __syncthreads();
+  for (int j = 0; j < QH_MAX; ++j) {
+    pin(v0[j]);
+    pin(v1[j]);
   }
-  const int n_parts = a.n_wparts + a.n_rparts;
-  float* R = a.rec + (seg * n_parts + part) * (int64_t)(g * (2 + D));
-  write_record_stats(sm.cs, R, g, tid);
-  for (int i = tid; i < g * D; i += NT) R[2 * g + i] = sm.ost[i];
 }
 
 // ------------------------------------------------------------------ retrieved role (VALU)
@@ -656,7 +982,7 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int64_t seg, int6
 // token rows; PV: sum_t p_ht b_tj from a per-tile nibble table of p applied to the
 // channel words.  The 4 waves' online-softmax partials are combined into one record.
 template <int T, int G4>
-__device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem<G4>& sm) {
+__device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem<G4>& sm, float* R) {
   constexpr int W = T / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -670,24 +996,29 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
   // wave 0 selects the tiles (when asked) while the other waves rotate query heads
   const int qw0 = a.do_select ? 1 : 0;
   if (a.do_select && wv_id == 0) {
-    topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sm.sel, sm.u.tk, lane);
+    select_tiles(a, seg, k, sm.sel, sm.u.tk, lane);
     wave_lds_sync();
     if (rp == 0)
       for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.sel[i];
   }
   if (wv_id >= qw0) {
-    for (int hh = wv_id - qw0; hh < G4; hh += 4 - qw0) {
-      float v0 = 0.f, v1 = 0.f;
-      if (hh < g) {
-        const int64_t qo = (b * a.Hq + h * g + hh) * D;
-        v0 = q_elem(a, qo + 2 * lane);
-        v1 = q_elem(a, qo + 2 * lane + 1);
-        rotate_pair(v0, v1, lane, a.transform, sm.xs[wv_id]);
+    float v0[QH_MAX], v1[QH_MAX];
+    load_heads(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
+#pragma unroll
+    for (int j = 0; j < QH_MAX; ++j) {
+      const int hh = wv_id - qw0 + (4 - qw0) * j;
+      if (hh < G4) {
+        float x0 = 0.f, x1 = 0.f;
+        if (hh < g) {
+          x0 = v0[j];
+          x1 = v1[j];
+          rotate_pair(x0, x1, lane, a.transform, sm.xs[wv_id]);
+        }
+        sm.qs[hh * D + 2 * lane] = x0;
+        sm.qs[hh * D + 2 * lane + 1] = x1;
+        const float tot = wave_sum(x0 + x1);
+        if (lane == 0) sm.qsum[hh] = tot;
       }
-      sm.qs[hh * D + 2 * lane] = v0;
-      sm.qs[hh * D + 2 * lane + 1] = v1;
-      const float tot = wave_sum(v0 + v1);
-      if (lane == 0) sm.qsum[hh] = tot;
     }
   }
   __syncthreads();
@@ -830,8 +1161,6 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
     }
     __syncthreads();
   }
-  const int n_parts = a.n_wparts + a.n_rparts;
-  float* R = a.rec + (seg * n_parts + a.n_wparts + rp) * (int64_t)(g * (2 + D));
   write_record_stats(sm.cs, R, g, tid);
   for (int i = tid; i < g * D; i += NT) R[2 * g + i] = sm.u.ost[i];
 }
@@ -839,16 +1168,20 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
 // ------------------------------------------------------------------ retrieved role (MFMA)
 
 struct RetMfmaSmem {
-  int32_t sel[TOPK_MAX_K];
-  u32x4 pm1[256];             // byte -> 8 fp16 values (+1 for a set bit, -1 otherwise)
-  u32x4 qb[4][2][64];         // Q'^T operands per k-step and fp16 part, per lane
-  float qs[16 * D];           // rotated query heads (zero beyond g)
-  float xs[4][D];
-  CombineSmem cs;
   union {
-    TopkSmem tk;
-    float ost[16 * D];
+    struct {
+      int32_t sel[TOPK_MAX_K];
+      u32x4 pm1[256];         // byte -> 8 fp16 values (+1 for a set bit, -1 otherwise)
+      u32x4 qb[4][2][64];     // Q'^T operands per k-step and fp16 part, per lane
+      float xs[4][D];
+      struct {
+        TopkSmem tk;          // wave 0's selection scratch (while the other waves fill qs)
+        float qs[16 * D];     // rotated query heads (zero beyond g)
+      } p;
+    };
+    float ow[4 * OW_WAVE];    // per-wave partial o' (after the tile loop)
   } u;
+  CombineSmem cs;
 };
 
 __device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
@@ -865,7 +1198,37 @@ __device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
 //     S^T accumulator slots are the PV k-slots (as in the window part); Vhat^T = +-1
 //     from two nibbles of the lane's channel word; sv*P split in 2 fp16 parts.
 template <int T>
-__device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm) {
+struct MfmaTile {
+  static constexpr int W = T / 64;
+  uint64_t kw[2][W];  // K channel words of channels lane and lane + 64 (bit-transpose rows)
+  uint64_t vw[8][W];  // V channel words of channels 16 cb + n
+  float sk, sv;
+};
+
+template <int T>
+__device__ __forceinline__ void fetch_mfma_tile(const DecodeArgs& a, int64_t seg, int64_t tile, int lane,
+                                                MfmaTile<T>& t) {
+  constexpr int W = T / 64;
+  const int n = lane & 15;
+  tile = tile < 0 ? 0 : (tile >= a.tile_stride ? a.tile_stride - 1 : tile);  // stay inside the store
+  const int64_t slot = seg * a.tile_stride + tile;
+  const uint64_t* kp = a.kbits + slot * (int64_t)(D * W);
+  const uint64_t* vp = a.vbits + slot * (int64_t)(D * W);
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    t.kw[0][w] = kp[lane * W + w];
+    t.kw[1][w] = kp[(lane + 64) * W + w];
+  }
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+    for (int w = 0; w < W; ++w) t.vw[cb][w] = vp[(16 * cb + n) * W + w];
+  t.sk = f16_to_f32(a.kscale[slot]) * SCALE_LOG2;
+  t.sv = f16_to_f32(a.vscale[slot]);
+}
+
+template <int T>
+__device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm, float* R) {
   constexpr int W = T / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -874,43 +1237,56 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int kg = lane >> 4;  // k-slot group
   const int g = a.g;
   const int k = a.k;
-  const int RS = a.n_rparts;
   const int64_t b = seg / a.Hkv;
   const int64_t h = seg - b * a.Hkv;
+
+  // Wave w takes the selected tiles j = rs*4 + w, then + 4*RS, ...; the first tile's
+  // words are fetched as soon as its index is known, each next one while the current
+  // tile is processed.
+  const int jstep = 4 * a.n_rparts;
+  const int j0 = rs * 4 + wv_id;
+  MfmaTile<T> cur;
+  if (!a.do_select && j0 < k) fetch_mfma_tile<T>(a, seg, a.idx[seg * k + j0], lane, cur);
 
   // wave 0 selects (when asked); waves 1..3 (or 0..3) rotate the query heads
   const int qw0 = a.do_select ? 1 : 0;
   if (a.do_select && wv_id == 0) {
-    topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sm.sel, sm.u.tk, lane);
+    select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane);
     wave_lds_sync();
     if (rs == 0)
-      for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.sel[i];
+      for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.u.sel[i];
   }
   if (wv_id >= qw0) {
-    for (int hh = wv_id - qw0; hh < 16; hh += 4 - qw0) {
-      float v0 = 0.f, v1 = 0.f;
-      if (hh < g) {
-        const int64_t qo = (b * a.Hq + h * g + hh) * D;
-        v0 = q_elem(a, qo + 2 * lane);
-        v1 = q_elem(a, qo + 2 * lane + 1);
-        rotate_pair(v0, v1, lane, a.transform, sm.xs[wv_id]);
+    float v0[QH_MAX], v1[QH_MAX];
+    load_heads(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
+#pragma unroll
+    for (int j = 0; j < QH_MAX; ++j) {
+      const int hh = wv_id - qw0 + (4 - qw0) * j;
+      if (hh < 16) {
+        float x0 = 0.f, x1 = 0.f;
+        if (hh < g) {
+          x0 = v0[j];
+          x1 = v1[j];
+          rotate_pair(x0, x1, lane, a.transform, sm.u.xs[wv_id]);
+        }
+        sm.u.p.qs[hh * D + 2 * lane] = x0;
+        sm.u.p.qs[hh * D + 2 * lane + 1] = x1;
       }
-      sm.qs[hh * D + 2 * lane] = v0;
-      sm.qs[hh * D + 2 * lane + 1] = v1;
     }
   }
   {  // +-1 patterns: entry x, element e = bit e of x
     const int x = tid;
     uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = ((x >> (2 * j)) & 1) ? 0x3c00u : 0xbc00u;      // fp16 +1 / -1
-      const uint32_t hi = ((x >> (2 * j + 1)) & 1) ? 0x3c00u : 0xbc00u;
-      w[j] = lo | (hi << 16);
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint32_t lo = ((x >> (2 * jj)) & 1) ? 0x3c00u : 0xbc00u;      // fp16 +1 / -1
+      const uint32_t hi = ((x >> (2 * jj + 1)) & 1) ? 0x3c00u : 0xbc00u;
+      w[jj] = lo | (hi << 16);
     }
-    sm.pm1[x] = u32x4{w[0], w[1], w[2], w[3]};
+    sm.u.pm1[x] = u32x4{w[0], w[1], w[2], w[3]};
   }
   __syncthreads();
+  if (a.do_select && j0 < k) fetch_mfma_tile<T>(a, seg, sm.u.sel[j0], lane, cur);  // in flight while Q' is built
 
   // Q'^T operands (B): lane (head n, kg), k-step ks: q'[n][32 ks + 8 kg + e], 2 fp16
   // parts; wave w builds k-step w into LDS (read back per tile, saving registers)
@@ -920,13 +1296,13 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       uint32_t pp[2];
-      split16<KVR_FP16, 2>(sm.qs[n * D + 32 * ks + 8 * kg + e], pp);
+      split16<KVR_FP16, 2>(sm.u.p.qs[n * D + 32 * ks + 8 * kg + e], pp);
       pe[0][e] = pp[0];
       pe[1][e] = pp[1];
     }
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp)
-      sm.qb[ks][sp][lane] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
+      sm.u.qb[ks][sp][lane] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
                                   pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
   }
   __syncthreads();
@@ -936,22 +1312,15 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   for (int i = 0; i < 8; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -__builtin_inff(), l_run = 0.f;
 
-  for (int j = rs * 4 + wv_id; j < k; j += 4 * RS) {
-    int64_t tile = a.do_select ? sm.sel[j] : a.idx[seg * k + j];
-    tile = tile < 0 ? 0 : (tile >= a.tile_stride ? a.tile_stride - 1 : tile);  // stay inside the store
-    const int64_t slot = seg * a.tile_stride + tile;
-    const uint64_t* kp = a.kbits + slot * (int64_t)(D * W);
-    const uint64_t* vp = a.vbits + slot * (int64_t)(D * W);
-    const float sk = f16_to_f32(a.kscale[slot]) * SCALE_LOG2;
-    const float sv = f16_to_f32(a.vscale[slot]);
-#pragma unroll 1
-    for (int w = 0; w < W; ++w) {
-      const uint64_t ka = kp[lane * W + w], kb = kp[(lane + 64) * W + w];
-      const uint32_t* vp32 = (const uint32_t*)vp;
-      uint32_t vw[8];  // dword 0 of the lane's channel words (tokens 0..31)
+  for (int j = j0; j < k; j += jstep) {
+    MfmaTile<T> nxt;  // the wave's next tile, fetched while this one is processed
+    if (j + jstep < k)
+      fetch_mfma_tile<T>(a, seg, a.do_select ? sm.u.sel[j + jstep] : a.idx[seg * k + j + jstep], lane, nxt);
+    const float sk = cur.sk, sv = cur.sv;
 #pragma unroll
-      for (int cb = 0; cb < 8; ++cb) vw[cb] = vp32[2 * ((16 * cb + n) * W + w)];
-      uint32_t row[4] = {(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)kb, (uint32_t)(kb >> 32)};
+    for (int w = 0; w < W; ++w) {
+      uint32_t row[4] = {(uint32_t)cur.kw[0][w], (uint32_t)(cur.kw[0][w] >> 32), (uint32_t)cur.kw[1][w],
+                         (uint32_t)(cur.kw[1][w] >> 32)};
       transpose64(row[0], row[1], lane);  // lane t: token t, channels 0..63
       transpose64(row[2], row[3], lane);  // channels 64..127
 
@@ -963,9 +1332,9 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const uint32_t d = (uint32_t)__shfl((int)row[ks], 16 * tb + n, 64);
-          const u32x4 av = sm.pm1[(d >> (8 * kg)) & 255u];
-          sacc[tb] = mfma16_f16(av, sm.qb[ks][0][lane], sacc[tb]);
-          sacc[tb] = mfma16_f16(av, sm.qb[ks][1][lane], sacc[tb]);
+          const u32x4 av = sm.u.pm1[(d >> (8 * kg)) & 255u];
+          sacc[tb] = mfma16_f16(av, sm.u.qb[ks][0][lane], sacc[tb]);
+          sacc[tb] = mfma16_f16(av, sm.u.qb[ks][1][lane], sacc[tb]);
         }
       }
       // ---- online softmax over the 64 tokens (head n lane-local)
@@ -991,7 +1360,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
 #pragma unroll
       for (int i = 0; i < 8; ++i) oacc[i] = oacc[i] * alpha;
 
-      // ---- O'^T += Vhat^T (sv P)^T, two k-steps of 32 tokens
+      // ---- O'^T += Vhat^T (sv P)^T, two k-steps of 32 tokens (dword ks2 of the words)
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
         u32x4 pb[2];
@@ -1009,61 +1378,39 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
             pb[sp] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
                            pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
         }
-        if (ks2 == 1) {  // dword 1 of the channel words (tokens 32..63)
-#pragma unroll
-          for (int cb = 0; cb < 8; ++cb) vw[cb] = vp32[2 * ((16 * cb + n) * W + w) + 1];
-        }
         const int sh0 = 4 * kg;
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) {
-          const uint32_t lo = (vw[cb] >> sh0) & 15u;
-          const uint32_t hi = (vw[cb] >> (sh0 + 16)) & 15u;
-          const u32x4 av = sm.pm1[lo | (hi << 4)];
+          const uint32_t vd = (uint32_t)(cur.vw[cb][w] >> (32 * ks2));
+          const uint32_t lo = (vd >> sh0) & 15u;
+          const uint32_t hi = (vd >> (sh0 + 16)) & 15u;
+          const u32x4 av = sm.u.pm1[lo | (hi << 4)];
           oacc[cb] = mfma16_f16(av, pb[0], oacc[cb]);
           oacc[cb] = mfma16_f16(av, pb[1], oacc[cb]);
         }
       }
     }
+    cur = nxt;
   }
 
-  // ---- combine the 4 waves into one record (o' in the rotated domain)
+  // ---- combine the 4 waves into one record (o' in the rotated domain); ow overlays
+  // all of the role's scratch, dead once every wave has left the tile loop
+  __syncthreads();
   l_run += xor16_f(l_run);
   l_run += xor32_f(l_run);
-  if (kg == 0) {
-    sm.cs.cm[wv_id][n] = m_run;
-    sm.cs.cl[wv_id][n] = l_run;
-  }
-  __syncthreads();  // also: wave 0's selection scratch is dead
-  float mx = -__builtin_inff();
-#pragma unroll
-  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm.cs.cm[w][n]);
-  const float fw = exp2f(m_run - ((mx == -__builtin_inff()) ? 0.f : mx));
-  for (int i = tid; i < 16 * D; i += NT) sm.u.ost[i] = 0.f;
-  __syncthreads();
-#pragma unroll 1
-  for (int w = 0; w < 4; ++w) {
-    if (wv_id == w && n < g) {
-#pragma unroll
-      for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sm.u.ost[n * D + 16 * cb + 4 * kg + r] += oacc[cb][r] * fw;
-    }
-    __syncthreads();
-  }
-  const int n_parts = a.n_wparts + a.n_rparts;
-  float* R = a.rec + (seg * n_parts + a.n_wparts + rs) * (int64_t)(g * (2 + D));
-  write_record_stats(sm.cs, R, g, tid);
-  for (int i = tid; i < g * D; i += NT) R[2 * g + i] = sm.u.ost[i];
+  // oacc[cb][r] of lane (n, kg) is channel 16 cb + 4 kg + r
+  combine_record(oacc, m_run, l_run, sm.u.ow, sm.cs, g, R,
+                 [](int i, int r, int kgv) { return 16 * i + 4 * kgv + r; });
 }
 
 // ------------------------------------------------------------------ merge
 
 // One wave per (sequence, query head): LSE-merge every partial record of its segment
-// (window parts in the original domain, retrieved parts rotated), rotate the
-// retrieved sum back, normalise, store.  Lane p first holds part p's weight so the
-// record loads of all parts can be in flight together.
+// (window parts in the original domain, retrieved parts rotated; their sum is rotated
+// back once), normalise, store.  Record loads are clamped and branch-free so a batch
+// of parts is in flight together.
 __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
-  constexpr int MAXP = 16;  // records loaded per batch (all in flight together)
+  constexpr int MAXP = 16;  // records loaded per batch
   __shared__ float xs[D];
   const int lane = threadIdx.x;
   const int g = a.g;
@@ -1081,7 +1428,7 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
     float pm[MAXP], pl[MAXP];
     float2 po[MAXP];
 #pragma unroll
-    for (int p = 0; p < MAXP; ++p) {  // branch-free: clamp the part, mask its weight below
+    for (int p = 0; p < MAXP; ++p) {
       const int pc = (p0 + p < n_parts) ? p0 + p : n_parts - 1;
       const float* R = R0 + pc * rs;
       pm[p] = R[i];
@@ -1124,41 +1471,68 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
 
 // ------------------------------------------------------------------ kernels
 
-// Score items with the query computed in-block: grid = segments x chunks of 64 tiles.
+// Score item: the query mean is computed in-block (wave 0) while the tile words load;
+// with a candidate array the item's tiles are also sorted (wave 0) into its list.
+struct ScoreSmem {
+  float qs[D];
+  float xs[D];
+  uint64_t lc[64];
+};
+
 template <int T>
-__global__ __launch_bounds__(NT) void select_score_kernel(DecodeArgs a) {
-  __shared__ float qs[D];
-  __shared__ float xs[D];
-  const int64_t seg = blockIdx.x / a.n_chunks;
-  const int64_t chunk = blockIdx.x - seg * a.n_chunks;
-  if (threadIdx.x < 64) qbar_wave(a, seg, qs, xs, threadIdx.x);
+__device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, ScoreSmem& sm) {
+  constexpr int TPI = score_tiles_per_item(T);
+  const int64_t t0 = chunk * TPI;
+  const int64_t t1 = (t0 + TPI < a.n_tiles) ? t0 + TPI : a.n_tiles;
+  // every load of the item is issued before any result is used
+  const int32_t lo = *(a.excl_lo ? a.excl_lo + seg : &g_zero_i32);
+  const int32_t hi = *(a.excl_hi ? a.excl_hi + seg : &g_zero_i32);
+  ScoreWords<T> sw;
+  score_load<T>(a.kbits, seg, a.tile_stride, t0, t1, sw);
+  if (threadIdx.x < 64) {
+    qbar_wave(a, seg, sm.qs, sm.xs, threadIdx.x);
+    sm.lc[threadIdx.x] = 0;
+  }
   __syncthreads();
-  const int64_t t0 = chunk * SCORE_TILES;
-  const int64_t t1 = (t0 + SCORE_TILES < a.n_tiles) ? t0 + SCORE_TILES : a.n_tiles;
-  const int32_t lo = a.excl_lo ? a.excl_lo[seg] : 0;
-  const int32_t hi = a.excl_hi ? a.excl_hi[seg] : 0;
-  score_tiles_block<T, 0>(qs, a.kbits, seg, a.n_tiles, a.tile_stride, t0, t1, lo, hi, a.scores);
+  score_compute<T, 0>(sm.qs, sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
+  if (a.cand) {
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      uint64_t v = sm.lc[threadIdx.x];
+      sort64_desc(v, threadIdx.x);
+      a.cand[(seg * a.n_chunks + chunk) * 64 + threadIdx.x] = v;
+    }
+  }
 }
 
-// Blocks [0, BH*n_rparts) are the retrieved items (segment-major; the long ones, so
-// they start first); the rest are the window items.
+// Launch 1 (selecting): the score items, grid = segments x items.
+template <int T>
+__global__ __launch_bounds__(NT) void select_score_kernel(DecodeArgs a) {
+  __shared__ ScoreSmem sm;
+  const int64_t seg = blockIdx.x / a.n_chunks;
+  score_item<T>(a, seg, blockIdx.x - seg * a.n_chunks, sm);
+}
+
+// Launch 2: per segment its n_rparts retrieved items (one selected tile per wave)
+// followed by its n_wparts window items; the latency-bound retrieved items run
+// between the streaming window items.
 template <int T, int WDT, int QS, int RM, int G4>
-__global__ __launch_bounds__(NT, 4) void attend_kernel(DecodeArgs a, int64_t BH) {
+__global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs a) {
   __shared__ union {
     WindowSmem win;
     RetSmem<G4> ret;
     RetMfmaSmem retm;
   } sm;
-  const int64_t n_r = BH * a.n_rparts;
-  if ((int64_t)blockIdx.x < n_r) {
-    const int64_t seg = blockIdx.x / a.n_rparts;
-    const int rs = (int)(blockIdx.x - seg * a.n_rparts);
-    if constexpr (RM == 0) retrieved_role_mfma<T>(a, seg, rs, sm.retm);
-    else retrieved_role<T, G4>(a, seg, rs, sm.ret);
+  const int parts = a.n_rparts + a.n_wparts;
+  const int64_t seg = blockIdx.x / parts;
+  const int p = (int)(blockIdx.x - seg * parts);
+  const int64_t rs = a.g * (2 + D);
+  if (p < a.n_rparts) {
+    float* R = a.rec + (seg * parts + a.n_wparts + p) * rs;
+    if constexpr (RM == 0) retrieved_role_mfma<T>(a, seg, p, sm.retm, R);
+    else retrieved_role<T, G4>(a, seg, p, sm.ret, R);
   } else {
-    const int64_t it = blockIdx.x - n_r;
-    const int64_t seg = it / a.n_wparts;
-    window_role<WDT, QS, 3>(a, seg, (int)(it - seg * a.n_wparts), sm.win);
+    window_role<WDT, QS, 3>(a, seg, p - a.n_rparts, sm.win);
   }
 }
 
@@ -1212,15 +1586,18 @@ __global__ __launch_bounds__(NT) void score_kernel(const float* __restrict__ qba
                                                    const int32_t* __restrict__ excl_lo,
                                                    const int32_t* __restrict__ excl_hi,
                                                    float* __restrict__ scores) {
+  constexpr int TPI = score_tiles_per_item(T);
   __shared__ float qs[D];
   const int64_t seg = blockIdx.x / n_chunks;
   const int64_t chunk = blockIdx.x - seg * n_chunks;
+  const int64_t t0 = chunk * TPI;
+  const int64_t t1 = (t0 + TPI < n_tiles) ? t0 + TPI : n_tiles;
+  ScoreWords<T> sw;
+  score_load<T>(kbits, seg, tile_stride, t0, t1, sw);
   if (threadIdx.x < D) qs[threadIdx.x] = qbar_rot[seg * D + threadIdx.x];
   __syncthreads();
-  const int64_t t0 = chunk * SCORE_TILES;
-  const int64_t t1 = (t0 + SCORE_TILES < n_tiles) ? t0 + SCORE_TILES : n_tiles;
-  score_tiles_block<T, METHOD>(qs, kbits, seg, n_tiles, tile_stride, t0, t1,
-                               excl_lo ? excl_lo[seg] : 0, excl_hi ? excl_hi[seg] : 0, scores);
+  score_compute<T, METHOD>(qs, sw, seg, n_tiles, t0, t1, excl_lo ? excl_lo[seg] : 0,
+                           excl_hi ? excl_hi[seg] : 0, scores);
 }
 
 __global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ scores, int64_t n,
@@ -1278,14 +1655,33 @@ __global__ __launch_bounds__(64) void gather_tiles_kernel(const uint64_t* __rest
 
 // ------------------------------------------------------------------ host launchers
 
-int n_window_parts(int64_t win_len) { return (win_len > 0) ? (int)((win_len + WIN_SPAN - 1) / WIN_SPAN) : 0; }
-constexpr int RET_TILES_PER_BLOCK = 16;  // selected tiles per retrieved item (4 per wave)
+// Window tokens per window item: one 32-token chunk per wave (128) unless the
+// segments x window are large enough to keep >= KVR_WIN_MIN_ITEMS window items with
+// longer spans (fewer partial records for the merge); at most 16 chunks per wave.
+int64_t window_span(int64_t BH, int64_t win_len) {
+  int64_t s = (BH * win_len) / ((int64_t)WIN_UNIT * KVR_WIN_MIN_ITEMS);
+  s = s < 1 ? 1 : (s > 16 ? 16 : s);
+  return s * WIN_UNIT;
+}
+int n_window_parts(int64_t BH, int64_t win_len) {
+  const int64_t span = window_span(BH, win_len);
+  return (win_len > 0) ? (int)((win_len + span - 1) / span) : 0;
+}
+constexpr int RET_TILES_PER_BLOCK = KVR_RET_TILES;  // selected tiles per retrieved item
 int n_retrieved_parts(int k) { return (k > 0) ? (k + RET_TILES_PER_BLOCK - 1) / RET_TILES_PER_BLOCK : 0; }
 
+// Partial records in the workspace: one per window item and per retrieved item.
 size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k) {
   const int g = Hq / Hkv;
-  const int64_t parts = n_window_parts(win_len) + n_retrieved_parts(k);
+  const int64_t parts = n_window_parts(B * Hkv, win_len) + n_retrieved_parts(k);
   return (size_t)(B * Hkv * (parts > 0 ? parts : 1) * g * (2 + D)) * sizeof(float);
+}
+
+// Sorted per-item candidate lists for the two-level selection (selecting, k <= 64).
+size_t cand_bytes(int64_t B, int Hkv, int64_t n_tiles, int k, int T) {
+  if (k <= 0 || k > 64 || n_tiles <= 0) return 0;
+  const int64_t tpi = score_tiles_per_item(T);
+  return (size_t)(B * Hkv * ((n_tiles + tpi - 1) / tpi) * 64) * sizeof(uint64_t);
 }
 
 hipError_t launch_query_prep(int qt, int tf, const void* q, int64_t B, int Hq, int Hkv,
@@ -1314,7 +1710,8 @@ hipError_t launch_query_prep(int qt, int tf, const void* q, int64_t B, int Hq, i
 hipError_t launch_score(int T, int method, const float* qbar_rot, const uint64_t* kbits, int64_t BH,
                         int64_t n_tiles, int64_t tile_stride, const int32_t* excl_lo,
                         const int32_t* excl_hi, float* scores, hipStream_t s) {
-  const int64_t n_chunks = (n_tiles + SCORE_TILES - 1) / SCORE_TILES;
+  const int64_t tpi = score_tiles_per_item(T);
+  const int64_t n_chunks = (n_tiles + tpi - 1) / tpi;
   const int64_t nblk = BH * n_chunks;
   if (nblk == 0) return hipSuccess;
 #define KVR_SC(TV, MV)                                                                           \
@@ -1346,13 +1743,15 @@ static int retrieve_method() {
   return (e && (e[0] == 'v' || e[0] == 'V')) ? 1 : 0;
 }
 
-// Full decode: [score launch when do_select] -> attend launch -> merge launch.
+// Full decode: [score launch when selecting] -> attend launch (retrieved + window
+// items) -> merge launch.
 hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
                          const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
                          const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
                          const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
                          const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
-                         float* scores, int32_t* idx, float* rec, void* out, int ot, hipStream_t s) {
+                         float* scores, uint64_t* cand, int32_t* idx, float* rec, void* out, int ot,
+                         hipStream_t s) {
   DecodeArgs a{};
   a.q = q;
   a.q_dtype = qt;
@@ -1379,10 +1778,12 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   a.scores = scores;
   a.idx = idx;
   a.rec = rec;
-  a.n_chunks = (int)((n_tiles + SCORE_TILES - 1) / SCORE_TILES);
-  a.n_wparts = n_window_parts(win_len);
+  a.n_chunks = (int)((n_tiles + score_tiles_per_item(T) - 1) / score_tiles_per_item(T));
+  a.n_wparts = n_window_parts(B * Hkv, win_len);
+  a.win_span = window_span(B * Hkv, win_len);
   a.n_rparts = n_retrieved_parts(k);
   a.do_select = (do_select && k > 0) ? 1 : 0;
+  a.cand = (a.do_select && k <= 64) ? cand : nullptr;
   a.ret_method = retrieve_method();
   a.out = out;
   const int64_t BH = B * Hkv;
@@ -1401,10 +1802,9 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   {
     const dim3 grid((unsigned)(BH * (a.n_wparts + a.n_rparts)));
     const bool same = (qt == wdt) || win_len == 0;
-    const int g = a.g;
-    const int gsel = (g <= 4) ? 4 : (g <= 8) ? 8 : 16;
+    const int gsel = (a.g <= 4) ? 4 : (a.g <= 8) ? 8 : 16;
 #define KVR_ATT(TV, WV, QSV, RMV, G4V) \
-  hipLaunchKernelGGL((attend_kernel<TV, WV, QSV, RMV, G4V>), grid, dim3(NT), 0, s, a, BH)
+  hipLaunchKernelGGL((attend_kernel<TV, WV, QSV, RMV, G4V>), grid, dim3(NT), 0, s, a)
 #define KVR_ATT_G(TV, WV, QSV)                        \
   if (a.ret_method == 0) KVR_ATT(TV, WV, QSV, 0, 4);  \
   else if (gsel == 4) KVR_ATT(TV, WV, QSV, 1, 4);     \
