@@ -47,6 +47,12 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #ifndef KVR_WIN_MIN_ITEMS
 #define KVR_WIN_MIN_ITEMS 256
 #endif
+#ifndef KVR_CAND_MAX
+#define KVR_CAND_MAX 64  // k up to which score items write sorted candidate lists (0: never)
+#endif
+#ifndef KVR_RET_FIRST
+#define KVR_RET_FIRST 1  // 1: all retrieved items first in the attend grid, else per segment
+#endif
 #ifndef KVR_RET_TILES
 #define KVR_RET_TILES 8  // selected tiles per retrieved item (a multiple of 4: one per wave per round)
 #endif
@@ -83,15 +89,36 @@ struct DecodeArgs {
 
 // ------------------------------------------------------------------ small helpers
 
-__device__ __forceinline__ float q_elem(const DecodeArgs& a, int64_t i) {
-  if (a.q_dtype == KVR_BF16) return load_as_f32<KVR_BF16>(a.q, i);
-  if (a.q_dtype == KVR_FP16) return load_as_f32<KVR_FP16>(a.q, i);
-  return load_as_f32<KVR_FP32>(a.q, i);
-}
-
 // Materialise a loaded value here: keeps the compiler from sinking a load into the
 // branch that uses it (which would serialise loads meant to be in flight together).
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
+
+// Query loads without conversion: the dtype branch holds loads only (nothing in it
+// waits), the raw bits are pinned once after all loads of a batch, then converted.
+// An element pair (even offset) is one 32-bit word for 16-bit dtypes, two for fp32.
+__device__ __forceinline__ void q_pair_raw(const DecodeArgs& a, int64_t off, uint32_t& r0, uint32_t& r1) {
+  if (a.q_dtype == KVR_FP32) {
+    const uint2 u = *(const uint2*)((const float*)a.q + off);
+    r0 = u.x;
+    r1 = u.y;
+  } else {
+    r0 = *(const uint32_t*)((const uint16_t*)a.q + off);
+    r1 = 0u;
+  }
+}
+__device__ __forceinline__ void q_pair_cvt(const DecodeArgs& a, uint32_t r0, uint32_t r1, float& v0, float& v1) {
+  if (a.q_dtype == KVR_FP32) {
+    v0 = __uint_as_float(r0);
+    v1 = __uint_as_float(r1);
+  } else if (a.q_dtype == KVR_BF16) {
+    v0 = __uint_as_float(r0 << 16);
+    v1 = __uint_as_float(r0 & 0xffff0000u);
+  } else {
+    v0 = f16_to_f32((uint16_t)(r0 & 0xffffu));
+    v1 = f16_to_f32((uint16_t)(r0 >> 16));
+  }
+}
 
 // LDS in-order completion within one wave (no block barrier).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -126,26 +153,32 @@ __device__ __forceinline__ void q_pair(const DecodeArgs& a, int64_t off, float& 
 }
 
 // Rotated GQA-mean query of a segment into qs[128] (one wave; lane = channel pair).
-// All g heads are loaded first (clamped, branch-free) so the loads are in flight together,
-// then summed in head order.
-__device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs, int lane) {
+// qbar_load issues the loads of all g heads (clamped, branch-free) so they are in flight
+// together; qbar_finish sums them in head order, divides by g once, rotates, stores.
+__device__ __forceinline__ void qbar_load(const DecodeArgs& a, int64_t seg, int lane, uint32_t* r0, uint32_t* r1) {
   const int64_t b = seg / a.Hkv;
   const int h = (int)(seg - b * a.Hkv);
   const int64_t q0 = (b * a.Hq + (int64_t)h * a.g) * D + 2 * lane;
-  float v0[16], v1[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) q_pair(a, q0 + (int64_t)(i < a.g ? i : 0) * D, v0[i], v1[i]);
+  for (int i = 0; i < 16; ++i) q_pair_raw(a, q0 + (int64_t)(i < a.g ? i : 0) * D, r0[i], r1[i]);
+}
+
+__device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, uint32_t* r1, float* qs, float* xs,
+                                            int lane) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    pin(v0[i]);
-    pin(v1[i]);
+    pin(r0[i]);
+    pin(r1[i]);
   }
-  float m0 = v0[0], m1 = v1[0];
+  float m0, m1;
+  q_pair_cvt(a, r0[0], r1[0], m0, m1);
 #pragma unroll
   for (int i = 1; i < 16; ++i) {
     if (i < a.g) {
-      m0 = m0 + v0[i];
-      m1 = m1 + v1[i];
+      float v0, v1;
+      q_pair_cvt(a, r0[i], r1[i], v0, v1);
+      m0 = m0 + v0;
+      m1 = m1 + v1;
     }
   }
   m0 = __fdiv_rn(m0, (float)a.g);
@@ -153,6 +186,12 @@ __device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs
   rotate_pair(m0, m1, lane, a.transform, xs);
   qs[2 * lane] = m0;
   qs[2 * lane + 1] = m1;
+}
+
+__device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs, int lane) {
+  uint32_t r0[16], r1[16];
+  qbar_load(a, seg, lane, r0, r1);
+  qbar_finish(a, r0, r1, qs, xs, lane);
 }
 
 // Selection candidate (score_key << 32) | (0xffffffff - tile): a larger value is a
@@ -178,12 +217,12 @@ __device__ __forceinline__ int count_bits(uint64_t w) {
   }
 }
 
-// 16-lane tree h = 8, 4, 2, 1 (every lane of the group ends with the same value).
+// 16-lane tree h = 8, 4, 2, 1 by DPP (every lane of the group ends with the same value).
 __device__ __forceinline__ float tree16(float p) {
-  p = p + shfl_xor_f(p, 8);
-  p = p + shfl_xor_f(p, 4);
-  p = p + shfl_xor_f(p, 2);
-  p = p + shfl_xor_f(p, 1);
+  p = p + xor_lane_f<8>(p);
+  p = p + xor_lane_f<4>(p);
+  p = p + xor_lane_f<2>(p);
+  p = p + xor_lane_f<1>(p);
   return p;
 }
 
@@ -255,10 +294,10 @@ __device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<
       dot = (k == 0) ? prod : dot + prod;
     }
     dot = tree16(dot);
-    cc += __shfl_xor(cc, 8, 64);
-    cc += __shfl_xor(cc, 4, 64);
-    cc += __shfl_xor(cc, 2, 64);
-    cc += __shfl_xor(cc, 1, 64);
+    cc += (int)xor_lane_u<8>((uint32_t)cc);
+    cc += (int)xor_lane_u<4>((uint32_t)cc);
+    cc += (int)xor_lane_u<2>((uint32_t)cc);
+    cc += (int)xor_lane_u<1>((uint32_t)cc);
     if (li == 0 && tile < t1) {
       const float cn = sqrt_rn((float)cc) + EPS;
       float sc = __fdiv_rn(dot, qn * cn);
@@ -700,25 +739,6 @@ struct WindowSmem {
 };
 static_assert(sizeof(uint16_t) * WIN_CHUNK * D == sizeof(float) * OW_WAVE, "ow[w] must overlay vstage[w]");
 
-// Eight consecutive query elements (16-byte aligned) as floats.
-__device__ __forceinline__ void q_load8(const DecodeArgs& a, int64_t off, float* x) {
-  if (a.q_dtype == KVR_FP32) {
-    const float4 u = *(const float4*)((const float*)a.q + off);
-    const float4 v = *(const float4*)((const float*)a.q + off + 4);
-    x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
-    x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
-  } else {
-    const u32x4 r = *(const u32x4*)((const uint16_t*)a.q + off);
-    const bool bf = a.q_dtype == KVR_BF16;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t lo = (uint16_t)(r[i] & 0xffffu), hi = (uint16_t)(r[i] >> 16);
-      x[2 * i] = bf ? bf16_to_f32(lo) : f16_to_f32(lo);
-      x[2 * i + 1] = bf ? bf16_to_f32(hi) : f16_to_f32(hi);
-    }
-  }
-}
-
 // Wait for this wave's outstanding vector-memory loads (including direct LDS loads).
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0)
 
@@ -774,10 +794,20 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
   u32x4 qb[QS][4];
   {
     const int64_t qoff = (b * a.Hq + h * g + (n < g ? n : 0)) * D;
+    uint32_t qr[4][8];  // raw query words: 4 pairs (16-bit) or 8 floats per k-step
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int pr = 0; pr < 4; ++pr) q_pair_raw(a, qoff + 32 * ks + 8 * kg + 2 * pr, qr[ks][2 * pr], qr[ks][2 * pr + 1]);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pin(qr[ks][e]);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       float x[8];
-      q_load8(a, qoff + 32 * ks + 8 * kg, x);
+#pragma unroll
+      for (int pr = 0; pr < 4; ++pr) q_pair_cvt(a, qr[ks][2 * pr], qr[ks][2 * pr + 1], x[2 * pr], x[2 * pr + 1]);
       uint32_t pe[QS][8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -890,16 +920,19 @@ constexpr int QH_MAX = 6;  // ceil(16 / 3): heads per wave when 3 waves share 16
 __device__ __forceinline__ void load_heads(const DecodeArgs& a, int64_t b, int64_t h, int h0, int step,
                                            int lane, float* v0, float* v1) {
   const int64_t base = (b * a.Hq + h * a.g) * D + 2 * lane;
+  uint32_t r0[QH_MAX], r1[QH_MAX];
 #pragma unroll
   for (int j = 0; j < QH_MAX; ++j) {
     const int hh = h0 + step * j;
-    q_pair(a, base + (int64_t)(hh < a.g ? hh : 0) * D, v0[j], v1[j]);
+    q_pair_raw(a, base + (int64_t)(hh < a.g ? hh : 0) * D, r0[j], r1[j]);
   }
 #pragma unroll
   for (int j = 0; j < QH_MAX; ++j) {
-    pin(v0[j]);
-    pin(v1[j]);
+    pin(r0[j]);
+    pin(r1[j]);
   }
+#pragma unroll
+  for (int j = 0; j < QH_MAX; ++j) q_pair_cvt(a, r0[j], r1[j], v0[j], v1[j]);
 }
 
 // ------------------------------------------------------------------ retrieved role (VALU)
@@ -1487,20 +1520,28 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, Scor
   // every load of the item is issued before any result is used
   const int32_t lo = *(a.excl_lo ? a.excl_lo + seg : &g_zero_i32);
   const int32_t hi = *(a.excl_hi ? a.excl_hi + seg : &g_zero_i32);
+  // The item's one-wave work (query prologue, sort) runs on wave blockIdx % 4, so the
+  // items resident on a CU spread it over the four SIMDs.  The query loads go first:
+  // loads complete in issue order, so the prologue can run while the words stream in.
+  const int lane = threadIdx.x & 63;
+  const bool helper = (int)(threadIdx.x >> 6) == (int)(blockIdx.x & 3);
+  uint32_t qv0[16], qv1[16];
+  if (helper) qbar_load(a, seg, lane, qv0, qv1);
+  asm volatile("" ::: "memory");
   ScoreWords<T> sw;
   score_load<T>(a.kbits, seg, a.tile_stride, t0, t1, sw);
-  if (threadIdx.x < 64) {
-    qbar_wave(a, seg, sm.qs, sm.xs, threadIdx.x);
-    sm.lc[threadIdx.x] = 0;
+  if (helper) {
+    qbar_finish(a, qv0, qv1, sm.qs, sm.xs, lane);
+    sm.lc[lane] = 0;
   }
   __syncthreads();
   score_compute<T, 0>(sm.qs, sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
   if (a.cand) {
     __syncthreads();
-    if (threadIdx.x < 64) {
-      uint64_t v = sm.lc[threadIdx.x];
-      sort64_desc(v, threadIdx.x);
-      a.cand[(seg * a.n_chunks + chunk) * 64 + threadIdx.x] = v;
+    if (helper) {
+      uint64_t v = sm.lc[lane];
+      sort64_desc(v, lane);
+      a.cand[(seg * a.n_chunks + chunk) * 64 + lane] = v;
     }
   }
 }
@@ -1524,8 +1565,22 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs
     RetMfmaSmem retm;
   } sm;
   const int parts = a.n_rparts + a.n_wparts;
-  const int64_t seg = blockIdx.x / parts;
-  const int p = (int)(blockIdx.x - seg * parts);
+  int64_t seg;
+  int p;
+  if (KVR_RET_FIRST) {  // blocks [0, BH*n_rparts): retrieved items, then the window items
+    const int64_t nr = (int64_t)(gridDim.x / parts) * a.n_rparts;
+    if ((int64_t)blockIdx.x < nr) {
+      seg = blockIdx.x / a.n_rparts;
+      p = (int)(blockIdx.x - seg * a.n_rparts);
+    } else {
+      const int64_t it = blockIdx.x - nr;
+      seg = it / a.n_wparts;
+      p = a.n_rparts + (int)(it - seg * a.n_wparts);
+    }
+  } else {
+    seg = blockIdx.x / parts;
+    p = (int)(blockIdx.x - seg * parts);
+  }
   const int64_t rs = a.g * (2 + D);
   if (p < a.n_rparts) {
     float* R = a.rec + (seg * parts + a.n_wparts + p) * rs;
@@ -1783,7 +1838,7 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   a.win_span = window_span(B * Hkv, win_len);
   a.n_rparts = n_retrieved_parts(k);
   a.do_select = (do_select && k > 0) ? 1 : 0;
-  a.cand = (a.do_select && k <= 64) ? cand : nullptr;
+  a.cand = (a.do_select && k <= KVR_CAND_MAX && k <= 64) ? cand : nullptr;
   a.ret_method = retrieve_method();
   a.out = out;
   const int64_t BH = B * Hkv;

@@ -105,8 +105,12 @@ __global__ __launch_bounds__(64) void encode_tiles_kernel(
     s1 = s1 + fabsf(y1[t]);
   }
   float a = s0 + s1;  // tree step j += j + 64
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) a = a + shfl_xor_f(a, m);
+  a = a + xor_lane_f<32>(a);  // stride-halving tree across lanes, DPP / permlane (no LDS)
+  a = a + xor_lane_f<16>(a);
+  a = a + xor_lane_f<8>(a);
+  a = a + xor_lane_f<4>(a);
+  a = a + xor_lane_f<2>(a);
+  a = a + xor_lane_f<1>(a);
   float mean = a * (1.0f / (float)(T * D));
   mean = (mean < FP16_MAX) ? mean : FP16_MAX;
   const uint32_t s16 = f32_to_f16_rne(mean);
