@@ -305,7 +305,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "kvr_decode_step (all launches of one step)",
                      "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": read_traffic("decode_step_decode32k_pmc.md"),
+                     "traffic": read_traffic("decode_step_decode32k.md"),
                      "algorithmic_bytes": total, "compressed_bytes": comp,
                      "compressed_gbps": round(comp / ms / 1e6, 1)},
         "cpu_baseline": cpu,
