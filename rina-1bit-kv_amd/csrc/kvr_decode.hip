@@ -94,11 +94,17 @@ struct DecodeArgs {
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
 
-// Query loads without conversion: the dtype branch holds loads only (nothing in it
-// waits), the raw bits are pinned once after all loads of a batch, then converted.
-// An element pair (even offset) is one 32-bit word for 16-bit dtypes, two for fp32.
+// Query loads without conversion: the raw bits are pinned once after all loads of a
+// batch, then converted.  An element pair (even offset) is one 32-bit word for 16-bit
+// dtypes, two for fp32.  QT is the query dtype when the kernel knows it (straight-line
+// loads, so the compiler's wait before the first use counts exactly the loads issued
+// after them), or Q_RUNTIME (a.q_dtype; each load sits in a dtype branch, and the
+// compiler then waits for every outstanding load before the first use).
+constexpr int Q_RUNTIME = -1;
+template <int QT = Q_RUNTIME>
 __device__ __forceinline__ void q_pair_raw(const DecodeArgs& a, int64_t off, uint32_t& r0, uint32_t& r1) {
-  if (a.q_dtype == KVR_FP32) {
+  const int qt = (QT == Q_RUNTIME) ? a.q_dtype : QT;
+  if (qt == KVR_FP32) {
     const uint2 u = *(const uint2*)((const float*)a.q + off);
     r0 = u.x;
     r1 = u.y;
@@ -107,11 +113,13 @@ __device__ __forceinline__ void q_pair_raw(const DecodeArgs& a, int64_t off, uin
     r1 = 0u;
   }
 }
+template <int QT = Q_RUNTIME>
 __device__ __forceinline__ void q_pair_cvt(const DecodeArgs& a, uint32_t r0, uint32_t r1, float& v0, float& v1) {
-  if (a.q_dtype == KVR_FP32) {
+  const int qt = (QT == Q_RUNTIME) ? a.q_dtype : QT;
+  if (qt == KVR_FP32) {
     v0 = __uint_as_float(r0);
     v1 = __uint_as_float(r1);
-  } else if (a.q_dtype == KVR_BF16) {
+  } else if (qt == KVR_BF16) {
     v0 = __uint_as_float(r0 << 16);
     v1 = __uint_as_float(r0 & 0xffff0000u);
   } else {
@@ -119,6 +127,10 @@ __device__ __forceinline__ void q_pair_cvt(const DecodeArgs& a, uint32_t r0, uin
     v1 = f16_to_f32((uint16_t)(r0 >> 16));
   }
 }
+
+// 2^x by the hardware v_exp_f32 (exact at 0 and -inf -> 0; results below the fp32
+// normal range flush to 0, immaterial inside a softmax).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // LDS in-order completion within one wave (no block barrier).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -155,28 +167,30 @@ __device__ __forceinline__ void q_pair(const DecodeArgs& a, int64_t off, float& 
 // Rotated GQA-mean query of a segment into qs[128] (one wave; lane = channel pair).
 // qbar_load issues the loads of all g heads (clamped, branch-free) so they are in flight
 // together; qbar_finish sums them in head order, divides by g once, rotates, stores.
+template <int QT>
 __device__ __forceinline__ void qbar_load(const DecodeArgs& a, int64_t seg, int lane, uint32_t* r0, uint32_t* r1) {
   const int64_t b = seg / a.Hkv;
   const int h = (int)(seg - b * a.Hkv);
   const int64_t q0 = (b * a.Hq + (int64_t)h * a.g) * D + 2 * lane;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) q_pair_raw(a, q0 + (int64_t)(i < a.g ? i : 0) * D, r0[i], r1[i]);
+  for (int i = 0; i < 16; ++i) q_pair_raw<QT>(a, q0 + (int64_t)(i < a.g ? i : 0) * D, r0[i], r1[i]);
 }
 
+template <int QT>
 __device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, uint32_t* r1, float* qs, float* xs,
                                             int lane) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     pin(r0[i]);
-    pin(r1[i]);
+    if (QT == Q_RUNTIME || QT == KVR_FP32) pin(r1[i]);  // r1 is a constant 0 for 16-bit dtypes
   }
   float m0, m1;
-  q_pair_cvt(a, r0[0], r1[0], m0, m1);
+  q_pair_cvt<QT>(a, r0[0], r1[0], m0, m1);
 #pragma unroll
   for (int i = 1; i < 16; ++i) {
     if (i < a.g) {
       float v0, v1;
-      q_pair_cvt(a, r0[i], r1[i], v0, v1);
+      q_pair_cvt<QT>(a, r0[i], r1[i], v0, v1);
       m0 = m0 + v0;
       m1 = m1 + v1;
     }
@@ -190,8 +204,8 @@ __device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, u
 
 __device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs, int lane) {
   uint32_t r0[16], r1[16];
-  qbar_load(a, seg, lane, r0, r1);
-  qbar_finish(a, r0, r1, qs, xs, lane);
+  qbar_load<Q_RUNTIME>(a, seg, lane, r0, r1);
+  qbar_finish<Q_RUNTIME>(a, r0, r1, qs, xs, lane);
 }
 
 // Selection candidate (score_key << 32) | (0xffffffff - tile): a larger value is a
@@ -201,7 +215,6 @@ __device__ __forceinline__ uint64_t pack_cand(uint32_t key, uint32_t tile) {
 }
 __device__ __forceinline__ uint32_t cand_tile(uint64_t v) { return 0xffffffffu - (uint32_t)v; }
 
-__device__ const int32_t g_zero_i32 = 0;  // exclusion bound when no range is given
 
 // ------------------------------------------------------------------ scoring
 
@@ -298,15 +311,22 @@ __device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<
     cc += (int)xor_lane_u<4>((uint32_t)cc);
     cc += (int)xor_lane_u<2>((uint32_t)cc);
     cc += (int)xor_lane_u<1>((uint32_t)cc);
-    if (li == 0 && tile < t1) {
-      const float cn = sqrt_rn((float)cc) + EPS;
-      float sc = __fdiv_rn(dot, qn * cn);
-      if (sc != sc) sc = -__builtin_inff();
-      if (tile >= lo && tile < hi) sc = -__builtin_inff();
-      scores[seg * n_tiles + tile] = sc;
-      if (lc) lc[grp + 16 * i] = pack_cand(score_key(sc), (uint32_t)tile);
+    if (li == 0) {
+      uint64_t cand = 0;  // pads below every real candidate
+      if (tile < t1) {
+        const float cn = sqrt_rn((float)cc) + EPS;
+        float sc = __fdiv_rn(dot, qn * cn);
+        if (sc != sc) sc = -__builtin_inff();
+        if (tile >= lo && tile < hi) sc = -__builtin_inff();
+        scores[seg * n_tiles + tile] = sc;
+        cand = pack_cand(score_key(sc), (uint32_t)tile);
+      }
+      if (lc) lc[grp + 16 * i] = cand;
     }
   }
+  if (lc && li == 0)
+#pragma unroll
+    for (int i = TPG; i < 4; ++i) lc[grp + 16 * i] = 0;  // items of fewer than 64 tiles
 }
 
 // ------------------------------------------------------------------ top-k (one wave)
@@ -695,7 +715,7 @@ __device__ __forceinline__ void combine_record(const f32x4 (&oacc)[8], float m_r
     const float muh = (mh == -__builtin_inff()) ? 0.f : mh;
     float lt = 0.f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) lt += cs.cl[v][tid] * exp2f(cs.cm[v][tid] - muh);
+    for (int v = 0; v < 4; ++v) lt += cs.cl[v][tid] * fast_exp2(cs.cm[v][tid] - muh);
     R[tid] = mh;
     R[g + tid] = lt;
   }
@@ -707,7 +727,7 @@ __device__ __forceinline__ void combine_record(const f32x4 (&oacc)[8], float m_r
     const float muh = (mh == -__builtin_inff()) ? 0.f : mh;
     float acc = 0.f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc += ow[v * OW_WAVE + d * 16 + hn] * exp2f(cs.cm[v][hn] - muh);
+    for (int v = 0; v < 4; ++v) acc += ow[v * OW_WAVE + d * 16 + hn] * fast_exp2(cs.cm[v][hn] - muh);
     R[2 * g + e] = acc;
   }
 }
@@ -722,7 +742,7 @@ __device__ void write_record_stats(const CombineSmem& cs, float* R, int g, int t
     const float muh = (mh == -__builtin_inff()) ? 0.f : mh;
     float lt = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) lt += cs.cl[w][tid] * exp2f(cs.cm[w][tid] - muh);
+    for (int w = 0; w < 4; ++w) lt += cs.cl[w][tid] * fast_exp2(cs.cm[w][tid] - muh);
     R[tid] = mh;
     R[g + tid] = lt;
   }
@@ -754,6 +774,7 @@ typedef void __attribute__((address_space(3))) * lds_ptr_t;
 // 8 (l%16) ..), both issued before the query is read.
 template <int WDT, int QS, int PS>
 __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
+  constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv_id = tid >> 6;
@@ -798,7 +819,7 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int pr = 0; pr < 4; ++pr) q_pair_raw(a, qoff + 32 * ks + 8 * kg + 2 * pr, qr[ks][2 * pr], qr[ks][2 * pr + 1]);
+      for (int pr = 0; pr < 4; ++pr) q_pair_raw<QT>(a, qoff + 32 * ks + 8 * kg + 2 * pr, qr[ks][2 * pr], qr[ks][2 * pr + 1]);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -807,7 +828,7 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
     for (int ks = 0; ks < 4; ++ks) {
       float x[8];
 #pragma unroll
-      for (int pr = 0; pr < 4; ++pr) q_pair_cvt(a, qr[ks][2 * pr], qr[ks][2 * pr + 1], x[2 * pr], x[2 * pr + 1]);
+      for (int pr = 0; pr < 4; ++pr) q_pair_cvt<QT>(a, qr[ks][2 * pr], qr[ks][2 * pr + 1], x[2 * pr], x[2 * pr + 1]);
       uint32_t pe[QS][8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -867,13 +888,13 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
     cmax = fmaxf(cmax, xor32_f(cmax));
     const float m_new = fmaxf(m_run, cmax);
     const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
+    const float alpha = fast_exp2(m_run - m_use);
     m_run = m_new;
     float p[8];
     float psum = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      p[e] = exp2f(l2[e] - m_use);
+      p[e] = fast_exp2(l2[e] - m_use);
       psum += p[e];
     }
     l_run = l_run * alpha + psum;
@@ -917,6 +938,7 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 // segment: channel pair 2 lane, 2 lane + 1; loads clamped to head 0 past g, all issued
 // before any is used.
 constexpr int QH_MAX = 6;  // ceil(16 / 3): heads per wave when 3 waves share 16 slots
+template <int QT>
 __device__ __forceinline__ void load_heads(const DecodeArgs& a, int64_t b, int64_t h, int h0, int step,
                                            int lane, float* v0, float* v1) {
   const int64_t base = (b * a.Hq + h * a.g) * D + 2 * lane;
@@ -924,7 +946,7 @@ __device__ __forceinline__ void load_heads(const DecodeArgs& a, int64_t b, int64
 #pragma unroll
   for (int j = 0; j < QH_MAX; ++j) {
     const int hh = h0 + step * j;
-    q_pair_raw(a, base + (int64_t)(hh < a.g ? hh : 0) * D, r0[j], r1[j]);
+    q_pair_raw<QT>(a, base + (int64_t)(hh < a.g ? hh : 0) * D, r0[j], r1[j]);
   }
 #pragma unroll
   for (int j = 0; j < QH_MAX; ++j) {
@@ -932,7 +954,7 @@ __device__ __forceinline__ void load_heads(const DecodeArgs& a, int64_t b, int64
     pin(r1[j]);
   }
 #pragma unroll
-  for (int j = 0; j < QH_MAX; ++j) q_pair_cvt(a, r0[j], r1[j], v0[j], v1[j]);
+  for (int j = 0; j < QH_MAX; ++j) q_pair_cvt<QT>(a, r0[j], r1[j], v0[j], v1[j]);
 }
 
 // ------------------------------------------------------------------ retrieved role (VALU)
@@ -1014,8 +1036,8 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int64_t seg, int6
 // dot_h(t) = sum_j q'_hj b_tj from the nibble table of q' applied to the transposed
 // token rows; PV: sum_t p_ht b_tj from a per-tile nibble table of p applied to the
 // channel words.  The 4 waves' online-softmax partials are combined into one record.
-template <int T, int G4>
-__device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem<G4>& sm, float* R) {
+template <int T, int G4, int QT>
+__device__ __forceinline__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem<G4>& sm, float* R) {
   constexpr int W = T / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1026,8 +1048,11 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
   const int64_t h = seg - b * a.Hkv;
   const int RS = a.n_rparts;
 
-  // wave 0 selects the tiles (when asked) while the other waves rotate query heads
+  // wave 0 selects the tiles (when asked) while the other waves rotate query heads;
+  // given indices are copied to LDS so every index read is an LDS read
   const int qw0 = a.do_select ? 1 : 0;
+  if (!a.do_select)
+    for (int i = tid; i < k; i += NT) sm.sel[i] = a.idx[seg * k + i];
   if (a.do_select && wv_id == 0) {
     select_tiles(a, seg, k, sm.sel, sm.u.tk, lane);
     wave_lds_sync();
@@ -1036,7 +1061,7 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
   }
   if (wv_id >= qw0) {
     float v0[QH_MAX], v1[QH_MAX];
-    load_heads(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
+    load_heads<QT>(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
 #pragma unroll
     for (int j = 0; j < QH_MAX; ++j) {
       const int hh = wv_id - qw0 + (4 - qw0) * j;
@@ -1068,7 +1093,7 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
   }
   TileWords<W> cur, nxt;
   const int j0 = rp * 4 + wv_id;
-  if (j0 < k) load_tile<T>(a, seg, a.do_select ? sm.sel[j0] : a.idx[seg * k + j0], lane, cur);
+  if (j0 < k) load_tile<T>(a, seg, sm.sel[j0], lane, cur);
   __syncthreads();
 
   float m_run[G4], l_lane[G4], o0[G4], o1[G4];
@@ -1084,7 +1109,7 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
 #pragma unroll 1
   for (int j = j0; j < k; j += 4 * RS) {
     if (j + 4 * RS < k)
-      load_tile<T>(a, seg, a.do_select ? sm.sel[j + 4 * RS] : a.idx[seg * k + j + 4 * RS], lane, nxt);
+      load_tile<T>(a, seg, sm.sel[j + 4 * RS], lane, nxt);
 #pragma unroll 1
     for (int w = 0; w < W; ++w) {
       uint32_t a_lo = (uint32_t)cur.k0[w], a_hi = (uint32_t)(cur.k0[w] >> 32);
@@ -1113,9 +1138,9 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
       for (int hh = 0; hh < G4; ++hh) {
         const float lg = cur.sk * (2.f * dot[hh] - sm.qsum[hh]) * SCALE_LOG2;
         const float m_new = fmaxf(m_run[hh], wave_max(lg));
-        alpha[hh] = exp2f(m_run[hh] - m_new);
+        alpha[hh] = fast_exp2(m_run[hh] - m_new);
         m_run[hh] = m_new;
-        const float p = exp2f(lg - m_new);
+        const float p = fast_exp2(lg - m_new);
         l_lane[hh] = l_lane[hh] * alpha[hh] + p;
         psum[hh] = wave_sum(p);
         ps[lane * G4 + hh] = p;
@@ -1186,7 +1211,7 @@ __device__ void retrieved_role(const DecodeArgs& a, int64_t seg, int rp, RetSmem
           float mx = -__builtin_inff();
 #pragma unroll
           for (int w2 = 0; w2 < 4; ++w2) mx = fmaxf(mx, sm.cs.cm[w2][hh]);
-          const float fw = exp2f(m_run[hh] - ((mx == -__builtin_inff()) ? 0.f : mx));
+          const float fw = fast_exp2(m_run[hh] - ((mx == -__builtin_inff()) ? 0.f : mx));
           sm.u.ost[hh * D + lane] += o0[hh] * fw;
           sm.u.ost[hh * D + lane + 64] += o1[hh] * fw;
         }
@@ -1260,7 +1285,7 @@ __device__ __forceinline__ void fetch_mfma_tile(const DecodeArgs& a, int64_t seg
   t.sv = f16_to_f32(a.vscale[slot]);
 }
 
-template <int T>
+template <int T, int QT>
 __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm, float* R) {
   constexpr int W = T / 64;
   const int tid = threadIdx.x;
@@ -1279,7 +1304,12 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int jstep = 4 * a.n_rparts;
   const int j0 = rs * 4 + wv_id;
   MfmaTile<T> cur;
-  if (!a.do_select && j0 < k) fetch_mfma_tile<T>(a, seg, a.idx[seg * k + j0], lane, cur);
+  if (!a.do_select) {
+    if (j0 < k) fetch_mfma_tile<T>(a, seg, a.idx[seg * k + j0], lane, cur);
+    // the tile loop reads every next index from LDS in both modes (one address space:
+    // an index read through a pointer that is LDS or global would be a FLAT load)
+    for (int i = tid; i < k; i += NT) sm.u.sel[i] = a.idx[seg * k + i];
+  }
 
   // wave 0 selects (when asked); waves 1..3 (or 0..3) rotate the query heads
   const int qw0 = a.do_select ? 1 : 0;
@@ -1291,7 +1321,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   }
   if (wv_id >= qw0) {
     float v0[QH_MAX], v1[QH_MAX];
-    load_heads(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
+    load_heads<QT>(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
 #pragma unroll
     for (int j = 0; j < QH_MAX; ++j) {
       const int hh = wv_id - qw0 + (4 - qw0) * j;
@@ -1348,7 +1378,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   for (int j = j0; j < k; j += jstep) {
     MfmaTile<T> nxt;  // the wave's next tile, fetched while this one is processed
     if (j + jstep < k)
-      fetch_mfma_tile<T>(a, seg, a.do_select ? sm.u.sel[j + jstep] : a.idx[seg * k + j + jstep], lane, nxt);
+      fetch_mfma_tile<T>(a, seg, sm.u.sel[j + jstep], lane, nxt);
     const float sk = cur.sk, sv = cur.sv;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
@@ -1381,12 +1411,12 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
       cmax = fmaxf(cmax, xor16_f(cmax));
       cmax = fmaxf(cmax, xor32_f(cmax));
       const float m_new = fmaxf(m_run, cmax);
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = fast_exp2(m_run - m_new);
       m_run = m_new;
       float psum = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        lg[e] = exp2f(lg[e] - m_new);
+        lg[e] = fast_exp2(lg[e] - m_new);
         psum += lg[e];
       }
       l_run = l_run * alpha + psum;
@@ -1473,7 +1503,7 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
     for (int p = 0; p < MAXP; ++p) Mb = fmaxf(Mb, pm[p]);
     const float Mn = fmaxf(M, Mb);
     const float mu = (Mn == -__builtin_inff()) ? 0.f : Mn;
-    const float sc = exp2f(M - mu);
+    const float sc = fast_exp2(M - mu);
     L *= sc;
     w0 *= sc;
     w1 *= sc;
@@ -1482,7 +1512,7 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
     M = Mn;
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
-      const float f = (p0 + p < n_parts) ? exp2f(pm[p] - mu) : 0.f;
+      const float f = (p0 + p < n_parts) ? fast_exp2(pm[p] - mu) : 0.f;
       const bool win = p0 + p < a.n_wparts;
       L += pl[p] * f;
       w0 += win ? po[p].x * f : 0.f;
@@ -1507,35 +1537,37 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
 // Score item: the query mean is computed in-block (wave 0) while the tile words load;
 // with a candidate array the item's tiles are also sorted (wave 0) into its list.
 struct ScoreSmem {
-  float qs[D];
-  float xs[D];
+  float qs[4][D];  // per wave
+  float xs[4][D];
   uint64_t lc[64];
 };
 
-template <int T>
+template <int T, int QT>
 __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, ScoreSmem& sm) {
   constexpr int TPI = score_tiles_per_item(T);
   const int64_t t0 = chunk * TPI;
   const int64_t t1 = (t0 + TPI < a.n_tiles) ? t0 + TPI : a.n_tiles;
   // every load of the item is issued before any result is used
-  const int32_t lo = *(a.excl_lo ? a.excl_lo + seg : &g_zero_i32);
-  const int32_t hi = *(a.excl_hi ? a.excl_hi + seg : &g_zero_i32);
-  // The item's one-wave work (query prologue, sort) runs on wave blockIdx % 4, so the
-  // items resident on a CU spread it over the four SIMDs.  The query loads go first:
-  // loads complete in issue order, so the prologue can run while the words stream in.
+  // (a value select, not a pointer select: a load through a pointer that may be
+  // global or constant is a FLAT load, and a pending FLAT load makes the compiler
+  // wait for every outstanding load at the next use of any of them)
+  const int32_t lo = a.excl_lo ? a.excl_lo[seg] : 0;
+  const int32_t hi = a.excl_hi ? a.excl_hi[seg] : 0;
+  // Every wave builds the query mean itself (straight-line loads from L2, issued first:
+  // loads complete in issue order, so the prologue runs while the words stream in) and
+  // scores its tiles as soon as its own words are in, with no block barrier before the
+  // sort.  The sort runs on wave blockIdx % 4, so the items resident on a CU spread it
+  // over the four SIMDs.
   const int lane = threadIdx.x & 63;
-  const bool helper = (int)(threadIdx.x >> 6) == (int)(blockIdx.x & 3);
+  const int wv = threadIdx.x >> 6;
+  const bool helper = wv == (int)(blockIdx.x & 3);
   uint32_t qv0[16], qv1[16];
-  if (helper) qbar_load(a, seg, lane, qv0, qv1);
-  asm volatile("" ::: "memory");
+  qbar_load<QT>(a, seg, lane, qv0, qv1);
   ScoreWords<T> sw;
   score_load<T>(a.kbits, seg, a.tile_stride, t0, t1, sw);
-  if (helper) {
-    qbar_finish(a, qv0, qv1, sm.qs, sm.xs, lane);
-    sm.lc[lane] = 0;
-  }
-  __syncthreads();
-  score_compute<T, 0>(sm.qs, sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
+  qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane);
+  wave_lds_sync();
+  score_compute<T, 0>(sm.qs[wv], sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
   if (a.cand) {
     __syncthreads();
     if (helper) {
@@ -1547,11 +1579,11 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, Scor
 }
 
 // Launch 1 (selecting): the score items, grid = segments x items.
-template <int T>
+template <int T, int QT>
 __global__ __launch_bounds__(NT) void select_score_kernel(DecodeArgs a) {
   __shared__ ScoreSmem sm;
   const int64_t seg = blockIdx.x / a.n_chunks;
-  score_item<T>(a, seg, blockIdx.x - seg * a.n_chunks, sm);
+  score_item<T, QT>(a, seg, blockIdx.x - seg * a.n_chunks, sm);
 }
 
 // Launch 2: per segment its n_rparts retrieved items (one selected tile per wave)
@@ -1584,8 +1616,9 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs
   const int64_t rs = a.g * (2 + D);
   if (p < a.n_rparts) {
     float* R = a.rec + (seg * parts + a.n_wparts + p) * rs;
-    if constexpr (RM == 0) retrieved_role_mfma<T>(a, seg, p, sm.retm, R);
-    else retrieved_role<T, G4>(a, seg, p, sm.ret, R);
+    constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
+    if constexpr (RM == 0) retrieved_role_mfma<T, QT>(a, seg, p, sm.retm, R);
+    else retrieved_role<T, G4, QT>(a, seg, p, sm.ret, R);
   } else {
     window_role<WDT, QS, 3>(a, seg, p - a.n_rparts, sm.win);
   }
@@ -1850,13 +1883,20 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   }
   if (a.do_select) {
     const dim3 grid((unsigned)(BH * a.n_chunks));
-    if (T == 64) hipLaunchKernelGGL(select_score_kernel<64>, grid, dim3(NT), 0, s, a);
-    else hipLaunchKernelGGL(select_score_kernel<128>, grid, dim3(NT), 0, s, a);
+#define KVR_SS(TV, QTV) \
+  if (T == TV && qt == QTV) hipLaunchKernelGGL((select_score_kernel<TV, QTV>), grid, dim3(NT), 0, s, a);
+    KVR_SS(64, KVR_BF16)
+    KVR_SS(64, KVR_FP16)
+    KVR_SS(64, KVR_FP32)
+    KVR_SS(128, KVR_BF16)
+    KVR_SS(128, KVR_FP16)
+    KVR_SS(128, KVR_FP32)
+#undef KVR_SS
     if (hipError_t e = hipGetLastError()) return e;
   }
   {
     const dim3 grid((unsigned)(BH * (a.n_wparts + a.n_rparts)));
-    const bool same = (qt == wdt) || win_len == 0;
+    const bool same = (qt == wdt);  // the QS = 1 instances take the query in the window dtype
     const int gsel = (a.g <= 4) ? 4 : (a.g <= 8) ? 8 : 16;
 #define KVR_ATT(TV, WV, QSV, RMV, G4V) \
   hipLaunchKernelGGL((attend_kernel<TV, WV, QSV, RMV, G4V>), grid, dim3(NT), 0, s, a)
