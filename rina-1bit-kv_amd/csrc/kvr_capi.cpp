@@ -26,9 +26,10 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
                          const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
                          const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
                          const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
-                         float* scores, uint64_t* cand, int32_t* idx, float* rec, void* out, int ot,
-                         hipStream_t s);
+                         float* scores, uint64_t* cand, int32_t* idx, float* rec, int32_t* ctr,
+                         void* out, int ot, hipStream_t s);
 size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k);
+size_t counter_bytes();
 size_t cand_bytes(int64_t B, int Hkv, int64_t n_tiles, int k, int T);
 hipError_t launch_gather(const uint64_t* bits, const uint16_t* scales, int64_t BH,
                          int64_t tile_stride, int T, int tf, const int32_t* idx, int k, float* out,
@@ -106,14 +107,17 @@ int check_store(const uint64_t* kb, const uint64_t* vb, const uint16_t* ks, cons
 }
 
 struct StepLayout {
-  size_t scores, cand, idx, rec, total;
+  size_t ctr, scores, cand, idx, rec, total;
 };
 
-// Workspace: [scores | candidate lists | idx | partial records]; plain scratch, no state
-// between calls.
+// Workspace: [counters | scores | candidate lists | idx | partial records].  The counter
+// region (same size and place in every decode workspace) must be zero before the
+// workspace's first call; every call leaves it zero.  The rest is scratch.
 StepLayout step_layout(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles, int k, int T) {
   StepLayout L{};
   size_t off = 0;
+  L.ctr = off;
+  off += round_up(kvr::counter_bytes());
   L.scores = off;
   off += round_up((size_t)(B * Hkv) * (size_t)(n_tiles > 0 ? n_tiles : 0) * sizeof(float));
   L.cand = off;
@@ -258,7 +262,8 @@ int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                                        win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
                                        kscale, vscale, 0, tile_stride, T, transform, nullptr, nullptr,
                                        k, false, nullptr, nullptr, const_cast<int32_t*>(idx),
-                                       (float*)(ws + L.rec), out, out_dtype, (hipStream_t)stream),
+                                       (float*)(ws + L.rec), nullptr, out, out_dtype,
+                                       (hipStream_t)stream),
                     "kvr_decode_attn");
 }
 
@@ -301,7 +306,8 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                                        kscale, vscale, n_tiles, tile_stride, T, transform, excl_lo,
                                        excl_hi, k, true, (float*)(ws + L.scores),
                                        (uint64_t*)(ws + L.cand), idx,
-                                       (float*)(ws + L.rec), out, out_dtype, (hipStream_t)stream),
+                                       (float*)(ws + L.rec), (int32_t*)(ws + L.ctr), out,
+                                       out_dtype, (hipStream_t)stream),
                     "kvr_decode_step");
 }
 

@@ -53,10 +53,30 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #ifndef KVR_RET_FIRST
 #define KVR_RET_FIRST 1  // 1: all retrieved items first in the attend grid, else per segment
 #endif
+#ifndef KVR_FUSED_STEP
+#define KVR_FUSED_STEP 1  // 1: the selecting step runs as one launch (step_kernel)
+#endif
+#ifndef KVR_STEP_ORDER
+// step_kernel block order after the score items: 0 all window items, then all retrieved
+// items; 1 the reverse; 2 per segment its window items, then its retrieved items
+#define KVR_STEP_ORDER 1
+#endif
+#ifndef KVR_SCORE_TPG
+#define KVR_SCORE_TPG 6  // tiles per 16-lane group of a score item at T = 64 (half at T = 128): 4, 6 or 8
+#endif
+#ifndef KVR_WIN_WAIT
+#define KVR_WIN_WAIT 1  // 1: step_kernel window items start once their segment's scores are done
+#endif
+#ifndef KVR_CTR_STRIDE
+#define KVR_CTR_STRIDE 32  // int32 words between per-segment counters (32: a 128-byte line each)
+#endif
 #ifndef KVR_RET_TILES
 #define KVR_RET_TILES 8  // selected tiles per retrieved item (a multiple of 4: one per wave per round)
 #endif
 
+// Segments (B * Hkv) up to which the selecting step runs as one launch; the counter
+// region at the start of every decode workspace holds their counters.
+constexpr int STEP_MAX_SEG = 4096;
 constexpr int WIN_CHUNK = 32;     // window tokens per wave per step
 constexpr int WIN_UNIT = 4 * WIN_CHUNK;  // window items span a multiple of this
 constexpr int TOPK_MAX_K = 1024;
@@ -80,6 +100,8 @@ struct DecodeArgs {
   uint64_t* cand;     // [BH][n_chunks][64] per-item candidates, sorted (k <= 64), or null
   int32_t* idx;       // [BH][k]
   float* rec;         // [BH][n_parts][g][2+D]
+  int32_t* ctr;       // fused step: work-queue header + per-segment counters (see step_kernel), or null
+  int64_t n_seg;      // B * Hkv
   int n_chunks, n_wparts, n_rparts;
   int64_t win_span;   // window tokens per window item
   int do_select;      // retrieved items select their tiles from scores (else read idx)
@@ -136,6 +158,23 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   __builtin_amdgcn_wave_barrier();
+}
+
+// Data handed from one block to another inside a launch (candidate lists, partial
+// records) is stored and loaded at agent scope: the stores write through to the
+// device-coherent level, so a block on another XCD reads it without an L2 write-back
+// or invalidate (agent-scope fences, which do those, cost far more than the data).
+__device__ __forceinline__ void rec_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float rec_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void cand_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t cand_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void rotate_pair(float& v0, float& v1, int lane, int tf, float* xs) {
@@ -240,17 +279,19 @@ __device__ __forceinline__ float tree16(float p) {
 }
 
 // Score items: 16 lanes per tile, lane li owns channels 8li..8li+7; each 16-lane group
-// scores TPG tiles (64 words in flight per lane for either T), so an item covers
-// 16*TPG tiles.  The words are loaded before the query is ready (one HBM round trip
-// per item, overlapped with the query prologue).
+// scores TPG tiles (16 * KVR_SCORE_TPG words in flight per lane for either T), so an
+// item covers 16*TPG tiles.  The words are loaded before the query is ready (one HBM
+// round trip per item, overlapped with the query prologue).
 template <int T>
 struct ScoreWords {
   static constexpr int W = T / 64;
-  static constexpr int TPG = 4 / W;
+  static constexpr int TPG = KVR_SCORE_TPG / W;
   uint64_t w[TPG][8 * W];
 };
 
-constexpr int score_tiles_per_item(int T) { return 16 * (4 / (T / 64)); }
+constexpr int score_tiles_per_item(int T) { return 16 * (KVR_SCORE_TPG / (T / 64)); }
+// Candidate slots of a score item (its tiles, padded to a multiple of 64).
+constexpr int score_cand_slots(int T) { return score_tiles_per_item(T) <= 64 ? 64 : 128; }
 
 template <int T>
 __device__ __forceinline__ void score_load(const uint64_t* kbits, int64_t seg, int64_t tile_stride,
@@ -326,7 +367,7 @@ __device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<
   }
   if (lc && li == 0)
 #pragma unroll
-    for (int i = TPG; i < 4; ++i) lc[grp + 16 * i] = 0;  // items of fewer than 64 tiles
+    for (int i = TPG; i < score_cand_slots(T) / 16; ++i) lc[grp + 16 * i] = 0;  // padding slots
 }
 
 // ------------------------------------------------------------------ top-k (one wave)
@@ -471,13 +512,13 @@ __device__ __forceinline__ uint64_t merge_top64(uint64_t a, uint64_t b_rev, int 
 __device__ __forceinline__ void select_from_cands(const uint64_t* lists, int n_lists, int k, int32_t* sel,
                                                   int lane) {
   constexpr int BATCH = 8;
-  uint64_t acc = lists[lane];
+  uint64_t acc = cand_load(lists + lane);
   for (int c0 = 1; c0 < n_lists; c0 += BATCH) {
     uint64_t b[BATCH];
 #pragma unroll
     for (int i = 0; i < BATCH; ++i) {
       const int c = (c0 + i < n_lists) ? c0 + i : n_lists - 1;
-      b[i] = lists[(int64_t)c * 64 + (63 - lane)];
+      b[i] = cand_load(lists + (int64_t)c * 64 + (63 - lane));
     }
 #pragma unroll
     for (int i = 0; i < BATCH; ++i)
@@ -716,8 +757,8 @@ __device__ __forceinline__ void combine_record(const f32x4 (&oacc)[8], float m_r
     float lt = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) lt += cs.cl[v][tid] * fast_exp2(cs.cm[v][tid] - muh);
-    R[tid] = mh;
-    R[g + tid] = lt;
+    rec_store(R + tid, mh);
+    rec_store(R + g + tid, lt);
   }
   for (int e = tid; e < g * D; e += NT) {
     const int hn = e >> 7, d = e & (D - 1);
@@ -728,7 +769,7 @@ __device__ __forceinline__ void combine_record(const f32x4 (&oacc)[8], float m_r
     float acc = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc += ow[v * OW_WAVE + d * 16 + hn] * fast_exp2(cs.cm[v][hn] - muh);
-    R[2 * g + e] = acc;
+    rec_store(R + 2 * g + e, acc);
   }
 }
 
@@ -743,8 +784,8 @@ __device__ void write_record_stats(const CombineSmem& cs, float* R, int g, int t
     float lt = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) lt += cs.cl[w][tid] * fast_exp2(cs.cm[w][tid] - muh);
-    R[tid] = mh;
-    R[g + tid] = lt;
+    rec_store(R + tid, mh);
+    rec_store(R + g + tid, lt);
   }
 }
 
@@ -1220,7 +1261,7 @@ __device__ __forceinline__ void retrieved_role(const DecodeArgs& a, int64_t seg,
     __syncthreads();
   }
   write_record_stats(sm.cs, R, g, tid);
-  for (int i = tid; i < g * D; i += NT) R[2 * g + i] = sm.u.ost[i];
+  for (int i = tid; i < g * D; i += NT) rec_store(R + 2 * g + i, sm.u.ost[i]);
 }
 
 // ------------------------------------------------------------------ retrieved role (MFMA)
@@ -1285,8 +1326,13 @@ __device__ __forceinline__ void fetch_mfma_tile(const DecodeArgs& a, int64_t seg
   t.sv = f16_to_f32(a.vscale[slot]);
 }
 
+// ready (fused step): wave 0 waits until *ready >= ready_target before it selects, while
+// the other waves rotate the query heads (null: the scores are complete already).
+__device__ void ctr_wait(int32_t* hdr, const int32_t* p, int target);
+
 template <int T, int QT>
-__device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm, float* R) {
+__device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm, float* R,
+                                    const int32_t* ready = nullptr, int ready_target = 0) {
   constexpr int W = T / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1314,6 +1360,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   // wave 0 selects (when asked); waves 1..3 (or 0..3) rotate the query heads
   const int qw0 = a.do_select ? 1 : 0;
   if (a.do_select && wv_id == 0) {
+    if (ready && lane == 0) ctr_wait(a.ctr, ready, ready_target);
     select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane);
     wave_lds_sync();
     if (rs == 0)
@@ -1468,20 +1515,14 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
 
 // ------------------------------------------------------------------ merge
 
-// One wave per (sequence, query head): LSE-merge every partial record of its segment
-// (window parts in the original domain, retrieved parts rotated; their sum is rotated
-// back once), normalise, store.  Record loads are clamped and branch-free so a batch
-// of parts is in flight together.
-__global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
+// One wave per (sequence, query head i of segment seg): LSE-merge every partial record
+// of the segment (window parts in the original domain, retrieved parts rotated; their
+// sum is rotated back once), normalise, store.  Record loads are clamped and
+// branch-free so a batch of parts is in flight together.
+__device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, float* xs) {
   constexpr int MAXP = 16;  // records loaded per batch
-  __shared__ float xs[D];
-  const int lane = threadIdx.x;
   const int g = a.g;
-  const int64_t bq = blockIdx.x;  // b * Hq + head
-  const int64_t b = bq / a.Hq;
-  const int hq = (int)(bq - b * a.Hq);
-  const int h = hq / g, i = hq - h * g;
-  const int64_t seg = b * a.Hkv + h;
+  const int64_t bq = (seg / a.Hkv) * a.Hq + (seg % a.Hkv) * g + i;  // b * Hq + head
   const int n_parts = a.n_wparts + a.n_rparts;
   const int64_t rs = g * (2 + D);
   const float* R0 = a.rec + seg * n_parts * rs;
@@ -1494,9 +1535,9 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
     for (int p = 0; p < MAXP; ++p) {
       const int pc = (p0 + p < n_parts) ? p0 + p : n_parts - 1;
       const float* R = R0 + pc * rs;
-      pm[p] = R[i];
-      pl[p] = R[g + i];
-      po[p] = *(const float2*)(R + 2 * g + i * D + 2 * lane);
+      pm[p] = rec_load(R + i);
+      pl[p] = rec_load(R + g + i);
+      po[p] = make_float2(rec_load(R + 2 * g + i * D + 2 * lane), rec_load(R + 2 * g + i * D + 2 * lane + 1));
     }
     float Mb = -__builtin_inff();
 #pragma unroll
@@ -1532,6 +1573,15 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
   }
 }
 
+__global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
+  __shared__ float xs[D];
+  const int64_t bq = blockIdx.x;  // b * Hq + head
+  const int64_t b = bq / a.Hq;
+  const int hq = (int)(bq - b * a.Hq);
+  const int h = hq / a.g;
+  merge_head(a, b * a.Hkv + h, hq - h * a.g, threadIdx.x, xs);
+}
+
 // ------------------------------------------------------------------ kernels
 
 // Score item: the query mean is computed in-block (wave 0) while the tile words load;
@@ -1539,11 +1589,11 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
 struct ScoreSmem {
   float qs[4][D];  // per wave
   float xs[4][D];
-  uint64_t lc[64];
+  uint64_t lc[128];
 };
 
 template <int T, int QT>
-__device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, ScoreSmem& sm) {
+__device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int helper_wave, ScoreSmem& sm) {
   constexpr int TPI = score_tiles_per_item(T);
   const int64_t t0 = chunk * TPI;
   const int64_t t1 = (t0 + TPI < a.n_tiles) ? t0 + TPI : a.n_tiles;
@@ -1556,11 +1606,11 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, Scor
   // Every wave builds the query mean itself (straight-line loads from L2, issued first:
   // loads complete in issue order, so the prologue runs while the words stream in) and
   // scores its tiles as soon as its own words are in, with no block barrier before the
-  // sort.  The sort runs on wave blockIdx % 4, so the items resident on a CU spread it
-  // over the four SIMDs.
+  // sort.  The sort runs on wave helper_wave (the item number mod 4), so the items
+  // resident on a CU spread it over the four SIMDs.
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const bool helper = wv == (int)(blockIdx.x & 3);
+  const bool helper = wv == helper_wave;
   uint32_t qv0[16], qv1[16];
   qbar_load<QT>(a, seg, lane, qv0, qv1);
   ScoreWords<T> sw;
@@ -1573,7 +1623,14 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, Scor
     if (helper) {
       uint64_t v = sm.lc[lane];
       sort64_desc(v, lane);
-      a.cand[(seg * a.n_chunks + chunk) * 64 + lane] = v;
+      if constexpr (score_cand_slots(T) == 128) {  // the top 64 of 128: sort the halves, merge
+        uint64_t u = sm.lc[64 + lane];
+        sort64_desc(u, lane);
+        const uint64_t ur = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(u >> 32), 63 - lane, 64) << 32) |
+                            (uint64_t)(uint32_t)__shfl((int)(uint32_t)u, 63 - lane, 64);
+        v = merge_top64(v, ur, lane);
+      }
+      cand_store(a.cand + (seg * a.n_chunks + chunk) * 64 + lane, v);
     }
   }
 }
@@ -1583,7 +1640,7 @@ template <int T, int QT>
 __global__ __launch_bounds__(NT) void select_score_kernel(DecodeArgs a) {
   __shared__ ScoreSmem sm;
   const int64_t seg = blockIdx.x / a.n_chunks;
-  score_item<T, QT>(a, seg, blockIdx.x - seg * a.n_chunks, sm);
+  score_item<T, QT>(a, seg, blockIdx.x - seg * a.n_chunks, (int)(blockIdx.x & 3), sm);
 }
 
 // Launch 2: per segment its n_rparts retrieved items (one selected tile per wave)
@@ -1623,6 +1680,123 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs
     window_role<WDT, QS, 3>(a, seg, p - a.n_rparts, sm.win);
   }
 }
+
+// ------------------------------------------------------------------ fused step (one launch)
+
+// The selecting decode step as one launch whose blocks are its work items, in block
+// order: every score item (segment-major), then the window and retrieved items.  A
+// retrieved item waits (bounded) until every score item of its segment has published
+// its candidate list.  Blocks are dispatched in block order on each XCD and every
+// score item comes before every retrieved item, so whatever keeps a score item from
+// being dispatched is itself a score item (which never waits): the waits end.  Each
+// window and retrieved item counts its record into its segment; the segment's last
+// record merges the segment and clears the segment's counters, which no other block
+// touches after that.  Block-to-block data (candidate lists, records) is stored and
+// loaded at agent scope, and a block waits for its stores (vmcnt 0) before it counts
+// them in.  Every counter is per segment (no device-wide hot spot).
+//
+// Counter region (int32) at offset 0 of every decode workspace, which must be zero
+// before a workspace's first call and which every call leaves zero: a header of
+// CTR_HDR words ([CTR_ERR]: set when a bounded wait gives up; sticky), then per
+// segment s < STEP_MAX_SEG the score items done and the records done, each counter in
+// a 128-byte line of its own (counters sharing a line serialise at the coherence
+// point under the polls and increments of many blocks).
+constexpr int CTR_HDR = 64;    // 256 bytes
+constexpr int CTR_STRIDE = KVR_CTR_STRIDE;  // int32 words per counter
+constexpr int CTR_ERR = 0;
+constexpr int SPIN_MAX = 1 << 20;  // polls of a bounded wait before it sets the error flag
+
+__device__ __forceinline__ int ctr_load(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ctr_add(int32_t* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ctr_store(int32_t* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// One thread: wait until *p >= target, polling at most SPIN_MAX times.
+__device__ void ctr_wait(int32_t* hdr, const int32_t* p, int target) {
+  for (int n = 0; ctr_load(p) < target; ++n) {
+    if (n == SPIN_MAX) {
+      ctr_store(hdr + CTR_ERR, 1);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+struct StepSmem {
+  union {
+    WindowSmem win;
+    RetMfmaSmem retm;
+    ScoreSmem sc;
+    float xs[4][D];  // merge
+  } u;
+  int last;
+};
+
+template <int T, int WDT, int QS>
+__global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a) {
+  __shared__ StepSmem sm;
+  constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
+  const int tid = threadIdx.x;
+  const int64_t S = a.n_seg;
+  const int64_t n_score = S * a.n_chunks, n_win = S * a.n_wparts, n_ret = S * a.n_rparts;
+  const int parts = a.n_wparts + a.n_rparts;
+  int32_t* sdone = a.ctr + CTR_HDR;                       // score items done, [seg * CTR_STRIDE]
+  int32_t* rdone = sdone + STEP_MAX_SEG * CTR_STRIDE;    // records done, [seg * CTR_STRIDE]
+  const int64_t it = blockIdx.x;
+  if (it < n_score) {
+    const int64_t seg = it / a.n_chunks;
+    score_item<T, QT>(a, seg, it - seg * a.n_chunks, (int)(it & 3), sm.u.sc);
+    wait_vm();  // candidate list stored
+    __syncthreads();
+    if (tid == 0) ctr_add(sdone + seg * CTR_STRIDE, 1);
+    return;
+  }
+  const int64_t j = it - n_score;
+  int64_t seg;
+  int wp, rp;  // window part, or retrieved part (wp < 0)
+  if (KVR_STEP_ORDER == 2) {
+    seg = j / parts;
+    const int p = (int)(j - seg * parts);
+    wp = p < a.n_wparts ? p : -1;
+    rp = p - a.n_wparts;
+  } else {
+    const bool win = (KVR_STEP_ORDER == 1) ? (j >= n_ret) : (j < n_win);
+    const int64_t jj = win ? ((KVR_STEP_ORDER == 1) ? j - n_ret : j) : ((KVR_STEP_ORDER == 1) ? j : j - n_win);
+    const int per = win ? a.n_wparts : a.n_rparts;
+    seg = jj / per;
+    wp = win ? (int)(jj - seg * per) : -1;
+    rp = win ? 0 : (int)(jj - seg * per);
+  }
+  if (wp >= 0) {
+    if (KVR_WIN_WAIT) {  // leave the memory to the segment's score items until they are done
+      if (tid == 0) ctr_wait(a.ctr, sdone + seg * CTR_STRIDE, a.n_chunks);
+      __syncthreads();
+    }
+    window_role<WDT, QS, 3>(a, seg, wp, sm.u.win);
+  } else {
+    float* R = a.rec + (seg * parts + a.n_wparts + rp) * (int64_t)(a.g * (2 + D));
+    retrieved_role_mfma<T, QT>(a, seg, rp, sm.u.retm, R, sdone + seg * CTR_STRIDE, a.n_chunks);
+  }
+  wait_vm();  // record stored
+  __syncthreads();
+  if (tid == 0) sm.last = ctr_add(rdone + seg * CTR_STRIDE, 1) == parts - 1;
+  __syncthreads();
+  if (sm.last) {
+    if (tid == 0) {  // every item of the segment is past its counters
+      ctr_store(sdone + seg * CTR_STRIDE, 0);
+      ctr_store(rdone + seg * CTR_STRIDE, 0);
+    }
+    const int w = tid >> 6;
+    for (int hh = w; hh < a.g; hh += 4) merge_head(a, seg, hh, tid & 63, sm.u.xs[w]);
+  }
+}
+
+// Bytes of the counter region that starts every decode workspace.
+size_t counter_bytes() { return (size_t)(CTR_HDR + 2 * STEP_MAX_SEG * CTR_STRIDE) * sizeof(int32_t); }
 
 // Output of segments with neither window tokens nor retrieved tiles: zeros.
 __global__ __launch_bounds__(NT) void zero_out_kernel(DecodeArgs a, int64_t n) {
@@ -1831,15 +2005,16 @@ static int retrieve_method() {
   return (e && (e[0] == 'v' || e[0] == 'V')) ? 1 : 0;
 }
 
-// Full decode: [score launch when selecting] -> attend launch (retrieved + window
-// items) -> merge launch.
+// Full decode.  Selecting with candidate lists: one launch (step_kernel).
+// Otherwise: [score launch when selecting] -> attend launch (retrieved + window items)
+// -> merge launch.
 hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
                          const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
                          const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
                          const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
                          const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
-                         float* scores, uint64_t* cand, int32_t* idx, float* rec, void* out, int ot,
-                         hipStream_t s) {
+                         float* scores, uint64_t* cand, int32_t* idx, float* rec, int32_t* ctr,
+                         void* out, int ot, hipStream_t s) {
   DecodeArgs a{};
   a.q = q;
   a.q_dtype = qt;
@@ -1874,11 +2049,28 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   a.cand = (a.do_select && k <= KVR_CAND_MAX && k <= 64) ? cand : nullptr;
   a.ret_method = retrieve_method();
   a.out = out;
+  a.ctr = ctr;
+  a.n_seg = B * Hkv;
   const int64_t BH = B * Hkv;
   if (BH == 0) return hipSuccess;
   if (a.n_wparts + a.n_rparts == 0) {
     const int64_t n = B * Hq * D;
     hipLaunchKernelGGL(zero_out_kernel, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, a, n);
+    return hipGetLastError();
+  }
+  if (KVR_FUSED_STEP && ctr && a.cand && a.ret_method == 0 && BH <= STEP_MAX_SEG) {
+    const int64_t tickets = BH * (a.n_chunks + a.n_wparts + a.n_rparts);  // blocks = work items
+    const bool same = (qt == wdt);
+#define KVR_ST(TV, WV, QSV) \
+  hipLaunchKernelGGL((step_kernel<TV, WV, QSV>), dim3((unsigned)tickets), dim3(NT), 0, s, a);
+#define KVR_ST_Q(TV, WV) \
+  if (same) KVR_ST(TV, WV, 1) else KVR_ST(TV, WV, 3)
+    if (T == 64 && wdt == KVR_FP16) { KVR_ST_Q(64, KVR_FP16) }
+    else if (T == 64) { KVR_ST_Q(64, KVR_BF16) }
+    else if (wdt == KVR_FP16) { KVR_ST_Q(128, KVR_FP16) }
+    else { KVR_ST_Q(128, KVR_BF16) }
+#undef KVR_ST_Q
+#undef KVR_ST
     return hipGetLastError();
   }
   if (a.do_select) {

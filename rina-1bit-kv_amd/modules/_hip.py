@@ -187,7 +187,7 @@ def decode_attn(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, idx, T, 
     wk, wv, wdt, wl, sb, sh, st = _window_args(win_k, win_v, win_len)
     need = lib().kvr_decode_attn_workspace(B, Hq, Hkv, wl, k, T)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)
+        workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=q.device)  # zeroed counter region
     out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
     tile_stride = kbits.shape[1] if kbits is not None else 1
     rc = lib().kvr_decode_attn(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, sb, sh, st,
@@ -198,10 +198,15 @@ def decode_attn(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, idx, T, 
     return out
 
 
+COUNTER_BYTES = 256 + 2 * 4096 * 128  # counter region at the start of every decode workspace
+
+
 def decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T, device):
-    """Workspace for decode_step (scores, indices, partial records; no initial contents needed)."""
+    """Workspace for decode_step / decode_attn.  It begins with the launch's counter region
+    (COUNTER_BYTES): zero before the first call, and every call leaves it zero; the rest is
+    scratch.  Reuse one workspace across calls on one stream, one per concurrent stream."""
     need = lib().kvr_decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T)
-    return torch.empty(max(need, 256), dtype=torch.uint8, device=device)
+    return torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
 
 
 def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles, T, transform, k,

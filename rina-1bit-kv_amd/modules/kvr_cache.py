@@ -103,8 +103,8 @@ class TileKVCache:
             need = _hip.lib().kvr_decode_step_workspace(self.B, q.shape[1], self.Hkv, self.n, self.n_tiles, k,
                                                         self.T)
             if self._ws is None or self._ws.numel() < need:
-                # grown geometrically; the kernels need no particular initial contents
-                self._ws = torch.empty(max(256, 2 * need), dtype=torch.uint8, device=self.device)
+                # grown geometrically; zeroed: it begins with the launch's counter region
+                self._ws = torch.zeros(max(256, 2 * need), dtype=torch.uint8, device=self.device)
             workspace = self._ws
         return _hip.decode_step(q, self.win_k, self.win_v, self.n, self.kbits, self.vbits, self.kscale,
                                 self.vscale, self.n_tiles, self.T, self.transform, k, out_dtype=out_dtype,

@@ -345,6 +345,41 @@ def test_decode_step_matches_oracle_pipeline(H, rng, tf, T, Hq, Hkv, ret_method)
     check_out(out, ref, "decode_step")
 
 
+def test_decode_step_workspace_reuse(H, rng):
+    """One workspace across calls of different shapes: its counter region is zero after
+    every call, the error flag included, and repeated calls give bit-identical outputs
+    (the merge order is fixed)."""
+    say("[decode_step/workspace reuse] counters stay zero; repeat calls bit-identical")
+    T, tf = 64, O.HADAMARD
+    ws = H.decode_step_workspace(4, 32, 8, 512, 64, 16, T, DEV)
+    outs = []
+    for B, Hkv, n_tiles, k, W in [(2, 8, 40, 6, 256), (4, 8, 64, 16, 512), (2, 8, 40, 6, 256), (1, 4, 33, 33, 0)]:
+        Hq = 4 * Hkv
+        gen = np.random.default_rng(7 + B + n_tiles)
+        K = torch.from_numpy(kv_like(gen, (B, Hkv, n_tiles * T, 128))).to(DEV, torch.bfloat16)
+        V = torch.from_numpy(gen.standard_normal((B, Hkv, n_tiles * T, 128)).astype(np.float32)).to(DEV, torch.bfloat16)
+        kb, ks = H.encode_tiles(K, T, tf)
+        vb, vs = H.encode_tiles(V, T, tf)
+        q = torch.from_numpy(gen.standard_normal((B, Hq, 128)).astype(np.float32)).to(DEV, torch.bfloat16)
+        wk = torch.from_numpy(kv_like(gen, (B, Hkv, max(W, 1), 128))).to(DEV, torch.bfloat16)
+        wv = torch.from_numpy(gen.standard_normal((B, Hkv, max(W, 1), 128)).astype(np.float32)).to(DEV, torch.bfloat16)
+        assert ws.numel() >= H.lib().kvr_decode_step_workspace(B, Hq, Hkv, W, n_tiles, k, T)
+        o1 = H.decode_step(q, wk, wv, W, kb, vb, ks, vs, n_tiles, T, tf, k, out_dtype=torch.float32, workspace=ws)
+        o2 = H.decode_step(q, wk, wv, W, kb, vb, ks, vs, n_tiles, T, tf, k, out_dtype=torch.float32, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2)
+        assert int(ws[:H.COUNTER_BYTES].count_nonzero().item()) == 0, ws[:16].cpu().numpy()
+        ig = torch.empty((B * Hkv, k), dtype=torch.int32, device=DEV)
+        H.decode_step(q, wk, wv, W, kb, vb, ks, vs, n_tiles, T, tf, k, out_dtype=torch.float32, idx_out=ig,
+                      workspace=ws)
+        qn = q.float().cpu().numpy()
+        ref = O.decode_attention(qn, wk.float().cpu().numpy()[:, :, :W], wv.float().cpu().numpy()[:, :, :W],
+                                 u64(kb), u64(vb), ks.cpu().numpy(), vs.cpu().numpy(), ig.cpu().numpy(), tf)
+        check_out(o1, ref, f"reuse B={B} n_tiles={n_tiles} k={k} W={W}")
+        outs.append(o1)
+    assert torch.equal(outs[0], outs[2])
+
+
 def test_decode_step_window_only(H, rng):
     say("[decode_step/window-only] n_tiles = 0")
     B, Hq, Hkv, W = 2, 32, 8, 100
