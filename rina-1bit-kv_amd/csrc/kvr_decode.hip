@@ -1274,8 +1274,7 @@ struct RetMfmaSmem {
       u32x4 qb[4][2][64];     // Q'^T operands per k-step and fp16 part, per lane
       float xs[4][D];
       struct {
-        TopkSmem tk;          // wave 0's selection scratch (while the other waves fill qs)
-        float qs[16 * D];     // rotated query heads (zero beyond g)
+        TopkSmem tk;          // wave 0's selection scratch (while the other waves fill qb)
       } p;
     };
     float ow[4 * OW_WAVE];    // per-wave partial o' (after the tile loop)
@@ -1379,8 +1378,15 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
           x1 = v1[j];
           rotate_pair(x0, x1, lane, a.transform, sm.u.xs[wv_id]);
         }
-        sm.u.p.qs[hh * D + 2 * lane] = x0;
-        sm.u.p.qs[hh * D + 2 * lane + 1] = x1;
+        // Q'^T operand (B) of head column hh: lane (hh, kg) of k-step ks holds
+        // q'[hh][32 ks + 8 kg + e], e < 8, in 2 fp16 parts; this lane's channels 2 lane,
+        // 2 lane + 1 are k-step lane / 16, slot group (lane / 4) % 4, word lane % 4
+        uint32_t p0[2], p1[2];
+        split16<KVR_FP16, 2>(x0, p0);
+        split16<KVR_FP16, 2>(x1, p1);
+        uint32_t* q32 = (uint32_t*)&sm.u.qb[lane >> 4][0][hh + 16 * ((lane >> 2) & 3)];
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp) q32[sp * 64 * 4 + (lane & 3)] = pack2(p0[sp], p1[sp]);
       }
     }
   }
@@ -1396,26 +1402,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     sm.u.pm1[x] = u32x4{w[0], w[1], w[2], w[3]};
   }
   __syncthreads();
-  if (a.do_select && j0 < k) fetch_mfma_tile<T>(a, seg, sm.u.sel[j0], lane, cur);  // in flight while Q' is built
-
-  // Q'^T operands (B): lane (head n, kg), k-step ks: q'[n][32 ks + 8 kg + e], 2 fp16
-  // parts; wave w builds k-step w into LDS (read back per tile, saving registers)
-  {
-    const int ks = wv_id;
-    uint32_t pe[2][8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      uint32_t pp[2];
-      split16<KVR_FP16, 2>(sm.u.p.qs[n * D + 32 * ks + 8 * kg + e], pp);
-      pe[0][e] = pp[0];
-      pe[1][e] = pp[1];
-    }
-#pragma unroll
-    for (int sp = 0; sp < 2; ++sp)
-      sm.u.qb[ks][sp][lane] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
-                                  pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
-  }
-  __syncthreads();
+  if (a.do_select && j0 < k) fetch_mfma_tile<T>(a, seg, sm.u.sel[j0], lane, cur);
 
   f32x4 oacc[8];
 #pragma unroll
