@@ -99,11 +99,11 @@ int kvr_score_tiles(const float* qbar_rot, const uint64_t* kbits, int64_t BH, in
 int kvr_topk_tiles(const float* scores, int64_t BH, int64_t n_tiles, int64_t score_stride, int k,
                    int32_t* idx, kvr_stream_t stream);
 
-/* Workspace bytes kvr_decode_attn needs for these sizes.  Decode workspaces (both
- * entry points) begin with a 1,048,832-byte counter region that must be zero before a
- * workspace's first call; every call leaves it zero (allocate zeroed once, then
- * reuse).  The rest is scratch with no state kept between calls.  Calls that run
- * concurrently need their own workspaces. */
+/* Workspace bytes kvr_decode_attn needs for these sizes.  A decode workspace (either
+ * entry point) must be zeroed before its first call and is then reused across calls;
+ * it begins with a 1,048,832-byte counter region the calls keep from one call to the
+ * next (its first int32 is a sticky error word, set if a bounded wait gave up); the
+ * rest is scratch.  Calls that run concurrently need their own workspaces. */
 size_t kvr_decode_attn_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T);
 
 /*
@@ -125,7 +125,7 @@ int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                     const int32_t* idx, int k, void* out, int out_dtype, void* workspace,
                     size_t ws_bytes, kvr_stream_t stream);
 
-/* Workspace bytes kvr_decode_step needs for these sizes (zeroed counter region as above). */
+/* Workspace bytes kvr_decode_step needs for these sizes (zeroed before first use, as above). */
 size_t kvr_decode_step_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles,
                                  int k, int T);
 

@@ -64,11 +64,11 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #ifndef KVR_SCORE_TPG
 #define KVR_SCORE_TPG 6  // tiles per 16-lane group of a score item at T = 64 (half at T = 128): 4, 6 or 8
 #endif
-#ifndef KVR_WIN_WAIT
-#define KVR_WIN_WAIT 1  // 1: step_kernel window items start once their segment's scores are done
-#endif
 #ifndef KVR_CTR_STRIDE
 #define KVR_CTR_STRIDE 32  // int32 words between per-segment counters (32: a 128-byte line each)
+#endif
+#ifndef KVR_RET_PARTS
+#define KVR_RET_PARTS 2  // fp16 parts of the retrieved MFMA operands q' and sv*P
 #endif
 #ifndef KVR_RET_TILES
 #define KVR_RET_TILES 8  // selected tiles per retrieved item (a multiple of 4: one per wave per round)
@@ -77,6 +77,7 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 // Segments (B * Hkv) up to which the selecting step runs as one launch; the counter
 // region at the start of every decode workspace holds their counters.
 constexpr int STEP_MAX_SEG = 4096;
+constexpr int CTR_ERR_WORD = 0;  // counter-region word set when a bounded wait gives up (sticky)
 constexpr int WIN_CHUNK = 32;     // window tokens per wave per step
 constexpr int WIN_UNIT = 4 * WIN_CHUNK;  // window items span a multiple of this
 constexpr int TOPK_MAX_K = 1024;
@@ -175,6 +176,33 @@ __device__ __forceinline__ void cand_store(uint64_t* p, uint64_t v) {
 }
 __device__ __forceinline__ uint64_t cand_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Candidate lists validate themselves: an entry is stored as two 8-byte halves, each
+// carrying a 32-bit tag of (epoch, segment, list) in its high word, so a reader that
+// finds the expected tag in both halves has this call's entry of that list, whenever
+// it reads -- no completion wait and counter on the writer's side, no poll before the
+// read.  The epoch is per segment (fused step: the segment's epoch word + 1, advanced
+// by the segment's merging item) or CAND_EPOCH_CHAIN when the lists are written by an
+// earlier launch.
+constexpr uint32_t CAND_EPOCH_CHAIN = 0xffffffffu;
+__device__ __forceinline__ uint32_t cand_tag(uint32_t epoch, int64_t seg, int list) {
+  uint32_t x = epoch * 0x9e3779b1u ^ (uint32_t)seg * 0x85ebca77u ^ (uint32_t)(list + 1) * 0xc2b2ae3du;
+  x ^= x >> 16;  // murmur3 finaliser
+  x *= 0x85ebca6bu;
+  x ^= x >> 13;
+  x *= 0xc2b2ae35u;
+  x ^= x >> 16;
+  return x ? x : 1u;  // never 0: zeroed memory is never a valid entry
+}
+__device__ __forceinline__ void cand_put(uint64_t* list, int e, uint64_t v, uint32_t tag) {
+  cand_store(list + 2 * e, ((uint64_t)tag << 32) | (v & 0xffffffffull));
+  cand_store(list + 2 * e + 1, ((uint64_t)tag << 32) | (v >> 32));
+}
+__device__ __forceinline__ uint64_t cand_get(const uint64_t* list, int e, uint32_t tag, bool& ok) {
+  const uint64_t lo = cand_load(list + 2 * e), hi = cand_load(list + 2 * e + 1);
+  ok = ok && (uint32_t)(lo >> 32) == tag && (uint32_t)(hi >> 32) == tag;
+  return (hi << 32) | (lo & 0xffffffffull);
 }
 
 __device__ __forceinline__ void rotate_pair(float& v0, float& v1, int lane, int tf, float* xs) {
@@ -507,22 +535,35 @@ __device__ __forceinline__ uint64_t merge_top64(uint64_t a, uint64_t b_rev, int 
   return v;
 }
 
-// sel[0..k) from the n_lists descending candidate lists of a segment (k <= 64): all
-// lists are loaded first (list i reversed for lanes, clamped), then merged in order.
+// sel[0..k) from the n_lists descending candidate lists of a segment (k <= 64), 128
+// words per list: a batch of lists is loaded (list 0 in lane order, the others
+// reversed for the merge, clamped), reloaded until every entry carries its tag (the
+// lists' writers may still be running; at most SPIN_MAX reloads, then *err = 1), then
+// merged in order.
+constexpr int SPIN_MAX = 1 << 20;  // polls of a bounded wait before it sets the error flag
 __device__ __forceinline__ void select_from_cands(const uint64_t* lists, int n_lists, int k, int32_t* sel,
-                                                  int lane) {
+                                                  int lane, uint32_t epoch, int64_t seg, int32_t* err) {
   constexpr int BATCH = 8;
-  uint64_t acc = cand_load(lists + lane);
-  for (int c0 = 1; c0 < n_lists; c0 += BATCH) {
+  uint64_t acc = 0;
+  for (int c0 = 0; c0 < n_lists; c0 += BATCH) {
     uint64_t b[BATCH];
+    for (int n = 0;; ++n) {
+      bool ok = true;
 #pragma unroll
-    for (int i = 0; i < BATCH; ++i) {
-      const int c = (c0 + i < n_lists) ? c0 + i : n_lists - 1;
-      b[i] = cand_load(lists + (int64_t)c * 64 + (63 - lane));
+      for (int i = 0; i < BATCH; ++i) {
+        const int c = (c0 + i < n_lists) ? c0 + i : n_lists - 1;
+        b[i] = cand_get(lists + (int64_t)c * 128, c == 0 ? lane : 63 - lane, cand_tag(epoch, seg, c), ok);
+      }
+      if (__all(ok)) break;
+      if (n == SPIN_MAX) {
+        if (err && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
     for (int i = 0; i < BATCH; ++i)
-      if (c0 + i < n_lists) acc = merge_top64(acc, b[i], lane);
+      if (c0 + i < n_lists) acc = (c0 + i == 0) ? b[i] : merge_top64(acc, b[i], lane);
   }
   if (lane < k) sel[lane] = (int32_t)cand_tile(acc);
 }
@@ -681,8 +722,10 @@ __device__ __forceinline__ void topk_wave(const float* row, int64_t n, int k, in
 // candidate lists when they were written (k <= 64), else by the wave select over the
 // segment's scores.
 __device__ __forceinline__ void select_tiles(const DecodeArgs& a, int64_t seg, int k, int32_t* sel,
-                                             TopkSmem& tk, int lane) {
-  if (a.cand) select_from_cands(a.cand + seg * a.n_chunks * (int64_t)64, a.n_chunks, k, sel, lane);
+                                             TopkSmem& tk, int lane, uint32_t epoch = CAND_EPOCH_CHAIN) {
+  if (a.cand)
+    select_from_cands(a.cand + seg * a.n_chunks * (int64_t)128, a.n_chunks, k, sel, lane, epoch, seg,
+                      a.ctr ? a.ctr + CTR_ERR_WORD : nullptr);
   else topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sel, tk, lane);
 }
 
@@ -1325,13 +1368,13 @@ __device__ __forceinline__ void fetch_mfma_tile(const DecodeArgs& a, int64_t seg
   t.sv = f16_to_f32(a.vscale[slot]);
 }
 
-// ready (fused step): wave 0 waits until *ready >= ready_target before it selects, while
-// the other waves rotate the query heads (null: the scores are complete already).
-__device__ void ctr_wait(int32_t* hdr, const int32_t* p, int target);
-
+// epoch_word (fused step): the segment's epoch word; wave 0 selects from the lists of
+// this call (epoch + 1), which the segment's score items may still be writing, while the
+// other waves rotate the query heads.  Null: lists of an earlier launch.
 template <int T, int QT>
 __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm, float* R,
-                                    const int32_t* ready = nullptr, int ready_target = 0) {
+                                    const int32_t* epoch_word = nullptr) {
+  constexpr int RP = KVR_RET_PARTS;  // fp16 parts of q' and sv*P
   constexpr int W = T / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1359,8 +1402,10 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   // wave 0 selects (when asked); waves 1..3 (or 0..3) rotate the query heads
   const int qw0 = a.do_select ? 1 : 0;
   if (a.do_select && wv_id == 0) {
-    if (ready && lane == 0) ctr_wait(a.ctr, ready, ready_target);
-    select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane);
+    const uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT) + 1u
+                                   : CAND_EPOCH_CHAIN;
+    select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane, ep);
     wave_lds_sync();
     if (rs == 0)
       for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.u.sel[i];
@@ -1381,12 +1426,12 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
         // Q'^T operand (B) of head column hh: lane (hh, kg) of k-step ks holds
         // q'[hh][32 ks + 8 kg + e], e < 8, in 2 fp16 parts; this lane's channels 2 lane,
         // 2 lane + 1 are k-step lane / 16, slot group (lane / 4) % 4, word lane % 4
-        uint32_t p0[2], p1[2];
-        split16<KVR_FP16, 2>(x0, p0);
-        split16<KVR_FP16, 2>(x1, p1);
+        uint32_t p0[RP], p1[RP];
+        split16<KVR_FP16, RP>(x0, p0);
+        split16<KVR_FP16, RP>(x1, p1);
         uint32_t* q32 = (uint32_t*)&sm.u.qb[lane >> 4][0][hh + 16 * ((lane >> 2) & 3)];
 #pragma unroll
-        for (int sp = 0; sp < 2; ++sp) q32[sp * 64 * 4 + (lane & 3)] = pack2(p0[sp], p1[sp]);
+        for (int sp = 0; sp < RP; ++sp) q32[sp * 64 * 4 + (lane & 3)] = pack2(p0[sp], p1[sp]);
       }
     }
   }
@@ -1430,8 +1475,8 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
         for (int ks = 0; ks < 4; ++ks) {
           const uint32_t d = (uint32_t)__shfl((int)row[ks], 16 * tb + n, 64);
           const u32x4 av = sm.u.pm1[(d >> (8 * kg)) & 255u];
-          sacc[tb] = mfma16_f16(av, sm.u.qb[ks][0][lane], sacc[tb]);
-          sacc[tb] = mfma16_f16(av, sm.u.qb[ks][1][lane], sacc[tb]);
+#pragma unroll
+          for (int sp = 0; sp < RP; ++sp) sacc[tb] = mfma16_f16(av, sm.u.qb[ks][sp][lane], sacc[tb]);
         }
       }
       // ---- online softmax over the 64 tokens (head n lane-local)
@@ -1460,18 +1505,18 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
       // ---- O'^T += Vhat^T (sv P)^T, two k-steps of 32 tokens (dword ks2 of the words)
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
-        u32x4 pb[2];
+        u32x4 pb[RP];
         {
-          uint32_t pe[2][8];
+          uint32_t pe[RP][8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            uint32_t pp[2];
-            split16<KVR_FP16, 2>(lg[8 * ks2 + e] * sv, pp);
-            pe[0][e] = pp[0];
-            pe[1][e] = pp[1];
+            uint32_t pp[RP];
+            split16<KVR_FP16, RP>(lg[8 * ks2 + e] * sv, pp);
+#pragma unroll
+            for (int sp = 0; sp < RP; ++sp) pe[sp][e] = pp[sp];
           }
 #pragma unroll
-          for (int sp = 0; sp < 2; ++sp)
+          for (int sp = 0; sp < RP; ++sp)
             pb[sp] = u32x4{pack2(pe[sp][0], pe[sp][1]), pack2(pe[sp][2], pe[sp][3]),
                            pack2(pe[sp][4], pe[sp][5]), pack2(pe[sp][6], pe[sp][7])};
         }
@@ -1482,8 +1527,8 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
           const uint32_t lo = (vd >> sh0) & 15u;
           const uint32_t hi = (vd >> (sh0 + 16)) & 15u;
           const u32x4 av = sm.u.pm1[lo | (hi << 4)];
-          oacc[cb] = mfma16_f16(av, pb[0], oacc[cb]);
-          oacc[cb] = mfma16_f16(av, pb[1], oacc[cb]);
+#pragma unroll
+          for (int sp = 0; sp < RP; ++sp) oacc[cb] = mfma16_f16(av, pb[sp], oacc[cb]);
         }
       }
     }
@@ -1580,7 +1625,8 @@ struct ScoreSmem {
 };
 
 template <int T, int QT>
-__device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int helper_wave, ScoreSmem& sm) {
+__device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int helper_wave, ScoreSmem& sm,
+                           uint32_t epoch = CAND_EPOCH_CHAIN) {
   constexpr int TPI = score_tiles_per_item(T);
   const int64_t t0 = chunk * TPI;
   const int64_t t1 = (t0 + TPI < a.n_tiles) ? t0 + TPI : a.n_tiles;
@@ -1617,7 +1663,7 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int 
                             (uint64_t)(uint32_t)__shfl((int)(uint32_t)u, 63 - lane, 64);
         v = merge_top64(v, ur, lane);
       }
-      cand_store(a.cand + (seg * a.n_chunks + chunk) * 64 + lane, v);
+      cand_put(a.cand + (seg * a.n_chunks + chunk) * 128, lane, v, cand_tag(epoch, seg, (int)chunk));
     }
   }
 }
@@ -1671,27 +1717,26 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs
 // ------------------------------------------------------------------ fused step (one launch)
 
 // The selecting decode step as one launch whose blocks are its work items, in block
-// order: every score item (segment-major), then the window and retrieved items.  A
-// retrieved item waits (bounded) until every score item of its segment has published
-// its candidate list.  Blocks are dispatched in block order on each XCD and every
-// score item comes before every retrieved item, so whatever keeps a score item from
-// being dispatched is itself a score item (which never waits): the waits end.  Each
-// window and retrieved item counts its record into its segment; the segment's last
-// record merges the segment and clears the segment's counters, which no other block
-// touches after that.  Block-to-block data (candidate lists, records) is stored and
-// loaded at agent scope, and a block waits for its stores (vmcnt 0) before it counts
-// them in.  Every counter is per segment (no device-wide hot spot).
+// order: every score item (segment-major), then the retrieved items, then the window
+// items (KVR_STEP_ORDER).  A retrieved item selects from its segment's candidate lists,
+// reloading until every entry carries this call's tag (the lists validate themselves,
+// see cand_tag): it waits only on score items, which precede it in block order, and
+// blocks are dispatched in block order on each XCD, so whatever keeps a score item
+// from being dispatched is itself a score item (which never waits) -- the waits end;
+// they are bounded anyway.  Each window and retrieved item counts its record into its
+// segment; the segment's last record merges the segment, clears its record counter and
+// advances its epoch (every item of the segment is done with both).  Partial records
+// are stored and loaded at agent scope, and a block waits for its record stores
+// (vmcnt 0) before it counts them in.  Every counter is per segment (no device-wide
+// hot spot).
 //
-// Counter region (int32) at offset 0 of every decode workspace, which must be zero
-// before a workspace's first call and which every call leaves zero: a header of
-// CTR_HDR words ([CTR_ERR]: set when a bounded wait gives up; sticky), then per
-// segment s < STEP_MAX_SEG the score items done and the records done, each counter in
-// a 128-byte line of its own (counters sharing a line serialise at the coherence
-// point under the polls and increments of many blocks).
+// Counter region (int32) at offset 0 of every decode workspace, zero before the
+// workspace's first call: a header of CTR_HDR words ([CTR_ERR_WORD]: set when a bounded
+// wait gives up; sticky), then per segment s < STEP_MAX_SEG its epoch and its records
+// done, each in a 128-byte line of its own (counters sharing a line serialise at the
+// coherence point under the loads and increments of many blocks).
 constexpr int CTR_HDR = 64;    // 256 bytes
 constexpr int CTR_STRIDE = KVR_CTR_STRIDE;  // int32 words per counter
-constexpr int CTR_ERR = 0;
-constexpr int SPIN_MAX = 1 << 20;  // polls of a bounded wait before it sets the error flag
 
 __device__ __forceinline__ int ctr_load(const int32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1701,16 +1746,6 @@ __device__ __forceinline__ int ctr_add(int32_t* p, int v) {
 }
 __device__ __forceinline__ void ctr_store(int32_t* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// One thread: wait until *p >= target, polling at most SPIN_MAX times.
-__device__ void ctr_wait(int32_t* hdr, const int32_t* p, int target) {
-  for (int n = 0; ctr_load(p) < target; ++n) {
-    if (n == SPIN_MAX) {
-      ctr_store(hdr + CTR_ERR, 1);
-      return;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
 }
 
 struct StepSmem {
@@ -1731,15 +1766,13 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a
   const int64_t S = a.n_seg;
   const int64_t n_score = S * a.n_chunks, n_win = S * a.n_wparts, n_ret = S * a.n_rparts;
   const int parts = a.n_wparts + a.n_rparts;
-  int32_t* sdone = a.ctr + CTR_HDR;                       // score items done, [seg * CTR_STRIDE]
-  int32_t* rdone = sdone + STEP_MAX_SEG * CTR_STRIDE;    // records done, [seg * CTR_STRIDE]
+  int32_t* epoch = a.ctr + CTR_HDR;                       // [seg * CTR_STRIDE] the segment's epoch
+  int32_t* rdone = epoch + STEP_MAX_SEG * CTR_STRIDE;    // [seg * CTR_STRIDE] records done
   const int64_t it = blockIdx.x;
   if (it < n_score) {
     const int64_t seg = it / a.n_chunks;
-    score_item<T, QT>(a, seg, it - seg * a.n_chunks, (int)(it & 3), sm.u.sc);
-    wait_vm();  // candidate list stored
-    __syncthreads();
-    if (tid == 0) ctr_add(sdone + seg * CTR_STRIDE, 1);
+    const uint32_t ep = (uint32_t)ctr_load(epoch + seg * CTR_STRIDE) + 1u;  // used when the list is stored
+    score_item<T, QT>(a, seg, it - seg * a.n_chunks, (int)(it & 3), sm.u.sc, ep);
     return;
   }
   const int64_t j = it - n_score;
@@ -1759,14 +1792,10 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a
     rp = win ? 0 : (int)(jj - seg * per);
   }
   if (wp >= 0) {
-    if (KVR_WIN_WAIT) {  // leave the memory to the segment's score items until they are done
-      if (tid == 0) ctr_wait(a.ctr, sdone + seg * CTR_STRIDE, a.n_chunks);
-      __syncthreads();
-    }
     window_role<WDT, QS, 3>(a, seg, wp, sm.u.win);
   } else {
     float* R = a.rec + (seg * parts + a.n_wparts + rp) * (int64_t)(a.g * (2 + D));
-    retrieved_role_mfma<T, QT>(a, seg, rp, sm.u.retm, R, sdone + seg * CTR_STRIDE, a.n_chunks);
+    retrieved_role_mfma<T, QT>(a, seg, rp, sm.u.retm, R, epoch + seg * CTR_STRIDE);
   }
   wait_vm();  // record stored
   __syncthreads();
@@ -1774,7 +1803,7 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a
   __syncthreads();
   if (sm.last) {
     if (tid == 0) {  // every item of the segment is past its counters
-      ctr_store(sdone + seg * CTR_STRIDE, 0);
+      ctr_add(epoch + seg * CTR_STRIDE, 1);
       ctr_store(rdone + seg * CTR_STRIDE, 0);
     }
     const int w = tid >> 6;
@@ -1930,7 +1959,7 @@ size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k) {
 size_t cand_bytes(int64_t B, int Hkv, int64_t n_tiles, int k, int T) {
   if (k <= 0 || k > 64 || n_tiles <= 0) return 0;
   const int64_t tpi = score_tiles_per_item(T);
-  return (size_t)(B * Hkv * ((n_tiles + tpi - 1) / tpi) * 64) * sizeof(uint64_t);
+  return (size_t)(B * Hkv * ((n_tiles + tpi - 1) / tpi) * 128) * sizeof(uint64_t);  // 64 entries x 2 tagged halves
 }
 
 hipError_t launch_query_prep(int qt, int tf, const void* q, int64_t B, int Hq, int Hkv,

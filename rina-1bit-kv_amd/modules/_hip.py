@@ -202,9 +202,10 @@ COUNTER_BYTES = 256 + 2 * 4096 * 128  # counter region at the start of every dec
 
 
 def decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T, device):
-    """Workspace for decode_step / decode_attn.  It begins with the launch's counter region
-    (COUNTER_BYTES): zero before the first call, and every call leaves it zero; the rest is
-    scratch.  Reuse one workspace across calls on one stream, one per concurrent stream."""
+    """Workspace for decode_step / decode_attn, zeroed: it begins with the launch's counter
+    region (COUNTER_BYTES; int32 word 0 is a sticky error word), which the calls keep from one
+    call to the next; the rest is scratch.  Reuse one workspace across calls on one stream,
+    one per concurrent stream."""
     need = lib().kvr_decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T)
     return torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
 

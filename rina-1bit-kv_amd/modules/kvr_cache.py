@@ -103,7 +103,7 @@ class TileKVCache:
             need = _hip.lib().kvr_decode_step_workspace(self.B, q.shape[1], self.Hkv, self.n, self.n_tiles, k,
                                                         self.T)
             if self._ws is None or self._ws.numel() < need:
-                # grown geometrically; zeroed: it begins with the launch's counter region
+                # grown geometrically; zeroed before its first call (it holds the launch's counters)
                 self._ws = torch.zeros(max(256, 2 * need), dtype=torch.uint8, device=self.device)
             workspace = self._ws
         return _hip.decode_step(q, self.win_k, self.win_v, self.n, self.kbits, self.vbits, self.kscale,
