@@ -33,6 +33,7 @@ from modules import _hip as H  # noqa: E402
 
 METRIC = "decode attn tokens/s @32k ctx b16; compressed-KV HBM GB/s vs roofline"
 HBM_PEAK_GBPS = 8000.0
+BF16_DENSE_TFLOPS = 2500.0  # MI355X dense bf16 MFMA peak
 D = 128
 
 
@@ -125,6 +126,10 @@ class DecodeWorkload:
         self._li = (self._li + 1) % len(self.layers)
         H.decode_step(self.q, wk, wv, self.W, kb, vb, ks, vs, self.n_tiles, self.T, self.transform, self.k,
                       out=self.out, idx_out=self.idx, workspace=self.ws)
+
+    def window_flops(self):
+        """MFMA work of the window part: QK and PV, 2 flop per multiply-add."""
+        return 4 * self.B * self.Hq * self.W * D
 
     def algorithmic_bytes(self):
         """Per step: all K bits scanned + K,V bits and fp16 scales of the selected tiles +
@@ -267,6 +272,7 @@ def main():
     ap.add_argument("--no-encode", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
     ap.add_argument("--no-rotate", action="store_true", help="skip the rotating-layers (HBM-resident) leg")
+    ap.add_argument("--no-cfg4", action="store_true", help="skip the configs[4] (DCT, T=128) decode leg")
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
 
@@ -299,6 +305,21 @@ def main():
         del wl.layers
         log(f"  decode step, 4 rotating layers (HBM-resident): {cold_ms * 1e3:.1f} us "
             f"({total / cold_ms / 1e6:.0f} GB/s algorithmic)")
+
+    # DCT-II, T=128, B=4, GQA 28/4, context 131072, window 2048, top-64 tiles
+    cfg4 = {}
+    if not args.no_cfg4:
+        log("building configs[4] workload (B=4, Hq=28, Hkv=4, N=131072, W=2048, T=128, k=64, DCT) ...")
+        wl4 = DecodeWorkload(B=4, Hq=28, Hkv=4, N=131072, W=2048, T=128, k=64, transform=H.DCT, seed=4)
+        ms4 = time_events(wl4.step, args.steps, args.warmup)
+        tot4, comp4 = wl4.algorithmic_bytes()
+        cfg4 = {"cfg4_us_per_step": round(ms4 * 1e3, 2), "cfg4_tokens_per_s": round(wl4.B / (ms4 / 1e3), 1),
+                "cfg4_algorithmic_bytes": tot4, "cfg4_gbps": round(tot4 / ms4 / 1e6, 1),
+                "cfg4_roofline_frac": round(tot4 / ms4 / 1e6 / HBM_PEAK_GBPS, 4)}
+        log(f"  configs[4] step {ms4 * 1e3:.1f} us ({tot4 / ms4 / 1e6:.0f} GB/s algorithmic, "
+            f"{cfg4['cfg4_roofline_frac'] * 100:.1f} % of 8 TB/s)")
+        del wl4
+        torch.cuda.empty_cache()
 
     breakdown = {} if args.no_breakdown else kernel_breakdown(wl, 50)
     if breakdown:
@@ -336,6 +357,10 @@ def main():
                      "compressed_gbps": round(comp / ms / 1e6, 1)},
         "cpu_baseline": cpu,
         "extra": {"planted_tile_recall": round(recall, 4),
+                  "tokens_per_s_32_layers": round(wl.B / (ms / 1e3) / 32, 1),
+                  "window_mfma_tflops": round(wl.window_flops() / ms / 1e9, 2),
+                  "window_mfma_util_vs_bf16_dense": round(wl.window_flops() / ms / 1e9 / BF16_DENSE_TFLOPS, 5),
+                  **cfg4,
                   "rotating_4_layers_us_per_step": round(cold_ms * 1e3, 2) if cold_ms else None,
                   "rotating_4_layers_gbps": round(total / cold_ms / 1e6, 1) if cold_ms else None, **enc,
                   **{k: round(v, 5) for k, v in breakdown.items()}},

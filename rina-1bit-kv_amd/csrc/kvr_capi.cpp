@@ -28,7 +28,7 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
                          const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
                          float* scores, uint64_t* cand, int32_t* idx, float* rec, int32_t* ctr,
                          void* out, int ot, hipStream_t s);
-size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k);
+size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T);
 size_t counter_bytes();
 size_t cand_bytes(int64_t B, int Hkv, int64_t n_tiles, int k, int T);
 hipError_t launch_gather(const uint64_t* bits, const uint16_t* scales, int64_t BH,
@@ -125,7 +125,7 @@ StepLayout step_layout(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_ti
   L.idx = off;
   off += round_up((size_t)(B * Hkv) * (size_t)(k > 0 ? k : 0) * sizeof(int32_t));
   L.rec = off;
-  off += round_up(kvr::records_bytes(B, Hq, Hkv, win_len, k));
+  off += round_up(kvr::records_bytes(B, Hq, Hkv, win_len, k, T));
   L.total = off;
   return L;
 }

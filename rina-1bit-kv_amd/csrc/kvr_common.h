@@ -203,43 +203,99 @@ constexpr DctTable make_dct_table() {
 static __constant__ DctTable g_dct_tab = make_dct_table();
 #define g_dct (g_dct_tab.v)
 
-// y = C x for a vector held as channels (2*lane, 2*lane+1); x is staged in
-// the caller's LDS buffer xs[128].  Tolerance path (fmaf allowed).
+// The entries of C as a 2 KB table: [r] = cos(pi r / 256) / 8 for r < 512 (C[k][n] for
+// k >= 1 is entry (2n+1) k mod 512, the same rounding as the matrix), [512] = C[0][n]
+// = sqrt(1/128); padded to a multiple of 4 floats.
+struct CosTable {
+  float v[516];
+};
+constexpr CosTable make_cos_table() {
+  CosTable t{};
+  for (int r = 0; r < 512; ++r) t.v[r] = (float)(0.125 * cos_pi_r256(r));
+  t.v[512] = (float)(0.088388347648318440550 * cos_pi_r256(0));
+  return t;
+}
+static __constant__ CosTable g_cos_tab = make_cos_table();
+
+// Floats of a wave's LDS scratch for dct_pair / idct_pair: the vector, then the table.
+constexpr int DCT_SCRATCH = D + 516;
+
+__device__ __forceinline__ void dct_table_to_lds(float* cs, int lane) {
+  const float4* src = (const float4*)g_cos_tab.v;
+  const float4 t0 = src[lane], t1 = src[lane + 64];
+  ((float4*)cs)[lane] = t0;
+  ((float4*)cs)[lane + 64] = t1;
+  if (lane == 0) ((float4*)cs)[128] = src[128];
+}
+
+// y = C x for a vector held as channels (2*lane, 2*lane+1), through the caller's
+// wave-private LDS scratch xs[DCT_SCRATCH].  C[k][127-n] = (-1)^k C[k][n], so with
+// s[n] = x[n] + x[127-n] and d[n] = x[n] - x[127-n] (n < 64) an even row is
+// sum_n C[k][n] s[n] and an odd row sum_n C[k][n] d[n]: 64 LDS table reads per output.
+// Tolerance path (fmaf, a different summation order than the plain product).
 __device__ __forceinline__ void dct_pair(float& v0, float& v1, int lane, float* xs) {
+  float* cs = xs + D;
+  dct_table_to_lds(cs, lane);
   xs[2 * lane] = v0;
   xs[2 * lane + 1] = v1;
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
+  const float xa = xs[lane], xb = xs[127 - lane];
+  __builtin_amdgcn_wave_barrier();
+  ((float2*)xs)[lane] = make_float2(xa + xb, xa - xb);  // (s[n], d[n]) at n = lane
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  // table index of C[k][n]: (2n+1) k mod 512, stepping by 2k; row 0 stays at 512
+  int r0 = lane == 0 ? 512 : 2 * lane;
+  const int d0 = lane == 0 ? 0 : 4 * lane, m0 = lane == 0 ? 1023 : 511;
+  int r1 = 2 * lane + 1;
+  const int d1 = 4 * lane + 2;
   float a0 = 0.f, a1 = 0.f;
-  const float* r0 = g_dct + (2 * lane) * D;
-  const float* r1 = r0 + D;
 #pragma unroll 8
-  for (int n = 0; n < D; ++n) {
-    float x = xs[n];
-    a0 = fmaf(r0[n], x, a0);
-    a1 = fmaf(r1[n], x, a1);
+  for (int n = 0; n < 64; ++n) {
+    const float2 sd = ((const float2*)xs)[n];
+    a0 = fmaf(cs[r0], sd.x, a0);
+    a1 = fmaf(cs[r1], sd.y, a1);
+    r0 = (r0 + d0) & m0;
+    r1 = (r1 + d1) & 511;
   }
   __builtin_amdgcn_wave_barrier();
   v0 = a0;
   v1 = a1;
 }
 
-// x = C^T y for a vector held as channels (2*lane, 2*lane+1).
+// x = C^T y for a vector held as channels (2*lane, 2*lane+1): lane n < 64 sums the even
+// rows E = sum C[2j][n] y[2j] and the odd rows O = sum C[2j+1][n] y[2j+1]; then
+// x[n] = E + O and x[127-n] = E - O.
 __device__ __forceinline__ void idct_pair(float& v0, float& v1, int lane, float* xs) {
+  float* cs = xs + D;
+  dct_table_to_lds(cs, lane);
   xs[2 * lane] = v0;
   xs[2 * lane + 1] = v1;
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
-  float a0 = 0.f, a1 = 0.f;
-#pragma unroll 8
-  for (int k = 0; k < D; ++k) {
-    float y = xs[k];
-    a0 = fmaf(g_dct[k * D + 2 * lane], y, a0);
-    a1 = fmaf(g_dct[k * D + 2 * lane + 1], y, a1);
+  const int st = 2 * lane + 1;  // 2n + 1
+  const float2 y01 = ((const float2*)xs)[0];
+  float e = cs[512] * y01.x;               // row 0
+  float o = cs[st] * y01.y;                // row 1
+  int re = (2 * st) & 511, ro = (3 * st) & 511;
+  const int dr = (2 * st) & 511;
+#pragma unroll 7
+  for (int j = 1; j < 64; ++j) {
+    const float2 y = ((const float2*)xs)[j];  // (y[2j], y[2j+1])
+    e = fmaf(cs[re], y.x, e);
+    o = fmaf(cs[ro], y.y, o);
+    re = (re + dr) & 511;
+    ro = (ro + dr) & 511;
   }
   __builtin_amdgcn_wave_barrier();
-  v0 = a0;
-  v1 = a1;
+  xs[lane] = e + o;
+  xs[127 - lane] = e - o;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  v0 = xs[2 * lane];
+  v1 = xs[2 * lane + 1];
+  __builtin_amdgcn_wave_barrier();
 }
 
 // Orderable key of an fp32 score: larger float -> larger key; NaN -> -inf.

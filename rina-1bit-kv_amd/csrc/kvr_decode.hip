@@ -541,18 +541,46 @@ __device__ __forceinline__ uint64_t merge_top64(uint64_t a, uint64_t b_rev, int 
 // lists' writers may still be running; at most SPIN_MAX reloads, then *err = 1), then
 // merged in order.
 constexpr int SPIN_MAX = 1 << 20;  // polls of a bounded wait before it sets the error flag
-__device__ __forceinline__ void select_from_cands(const uint64_t* lists, int n_lists, int k, int32_t* sel,
-                                                  int lane, uint32_t epoch, int64_t seg, int32_t* err) {
+
+// Waits until one word (the last) of every list c = first + step * i < n_lists carries
+// its tag: one 8-byte load per list and poll, so a waiting wave adds little traffic
+// while the lists' writers run.  At most SPIN_MAX polls, then *err = 1.
+__device__ __forceinline__ void probe_list_set(const uint64_t* lists, int first, int step, int n_lists,
+                                               int lane, uint32_t epoch, int64_t seg, int32_t* err) {
+  for (int r0 = first; r0 < n_lists; r0 += 64 * step) {
+    const int c = r0 + step * lane;
+    const uint32_t tag = cand_tag(epoch, seg, c);
+    for (int n = 0;; ++n) {
+      const bool ok = c >= n_lists || (uint32_t)(cand_load(lists + (int64_t)c * 128 + 127) >> 32) == tag;
+      if (__all(ok)) break;
+      if (n == SPIN_MAX) {
+        if (err && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+}
+
+// Top 64 (descending, lane order; 0 pads) of the lists c = first + step * i < n_lists of
+// a segment (128 words per list), loaded in batches of 8 (the first list in lane order,
+// the others reversed for the merge) and reloaded until every entry carries its tag
+// (the lists' writers may still be running; at most SPIN_MAX reloads, then *err = 1).
+// The full loads start once probe_list_set has seen every list's last word.
+__device__ __forceinline__ uint64_t merge_list_set(const uint64_t* lists, int first, int step, int n_lists,
+                                                   int lane, uint32_t epoch, int64_t seg, int32_t* err) {
   constexpr int BATCH = 8;
+  if (epoch != CAND_EPOCH_CHAIN) probe_list_set(lists, first, step, n_lists, lane, epoch, seg, err);
   uint64_t acc = 0;
-  for (int c0 = 0; c0 < n_lists; c0 += BATCH) {
+  for (int c0 = first; c0 < n_lists; c0 += BATCH * step) {
     uint64_t b[BATCH];
     for (int n = 0;; ++n) {
       bool ok = true;
 #pragma unroll
       for (int i = 0; i < BATCH; ++i) {
-        const int c = (c0 + i < n_lists) ? c0 + i : n_lists - 1;
-        b[i] = cand_get(lists + (int64_t)c * 128, c == 0 ? lane : 63 - lane, cand_tag(epoch, seg, c), ok);
+        const int c = (c0 + i * step < n_lists) ? c0 + i * step : c0;
+        b[i] = cand_get(lists + (int64_t)c * 128, (c0 == first && i == 0) ? lane : 63 - lane,
+                        cand_tag(epoch, seg, c), ok);
       }
       if (__all(ok)) break;
       if (n == SPIN_MAX) {
@@ -563,8 +591,16 @@ __device__ __forceinline__ void select_from_cands(const uint64_t* lists, int n_l
     }
 #pragma unroll
     for (int i = 0; i < BATCH; ++i)
-      if (c0 + i < n_lists) acc = (c0 + i == 0) ? b[i] : merge_top64(acc, b[i], lane);
+      if (c0 + i * step < n_lists) acc = (c0 == first && i == 0) ? b[i] : merge_top64(acc, b[i], lane);
   }
+  return acc;
+}
+
+// sel[0..k) from the n_lists descending candidate lists of a segment (k <= 64), merged by
+// one wave.
+__device__ __forceinline__ void select_from_cands(const uint64_t* lists, int n_lists, int k, int32_t* sel,
+                                                  int lane, uint32_t epoch, int64_t seg, int32_t* err) {
+  const uint64_t acc = merge_list_set(lists, 0, 1, n_lists, lane, epoch, seg, err);
   if (lane < k) sel[lane] = (int32_t)cand_tile(acc);
 }
 
@@ -1023,22 +1059,32 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 // before any is used.
 constexpr int QH_MAX = 6;  // ceil(16 / 3): heads per wave when 3 waves share 16 slots
 template <int QT>
-__device__ __forceinline__ void load_heads(const DecodeArgs& a, int64_t b, int64_t h, int h0, int step,
-                                           int lane, float* v0, float* v1) {
+__device__ __forceinline__ void load_heads_raw(const DecodeArgs& a, int64_t b, int64_t h, int h0, int step,
+                                               int lane, uint32_t* r0, uint32_t* r1) {
   const int64_t base = (b * a.Hq + h * a.g) * D + 2 * lane;
-  uint32_t r0[QH_MAX], r1[QH_MAX];
 #pragma unroll
   for (int j = 0; j < QH_MAX; ++j) {
     const int hh = h0 + step * j;
     q_pair_raw<QT>(a, base + (int64_t)(hh < a.g ? hh : 0) * D, r0[j], r1[j]);
   }
+}
+template <int QT>
+__device__ __forceinline__ void load_heads_cvt(const DecodeArgs& a, uint32_t* r0, uint32_t* r1, float* v0,
+                                               float* v1) {
 #pragma unroll
   for (int j = 0; j < QH_MAX; ++j) {
     pin(r0[j]);
-    pin(r1[j]);
+    if (QT == Q_RUNTIME || QT == KVR_FP32) pin(r1[j]);
   }
 #pragma unroll
   for (int j = 0; j < QH_MAX; ++j) q_pair_cvt<QT>(a, r0[j], r1[j], v0[j], v1[j]);
+}
+template <int QT>
+__device__ __forceinline__ void load_heads(const DecodeArgs& a, int64_t b, int64_t h, int h0, int step,
+                                           int lane, float* v0, float* v1) {
+  uint32_t r0[QH_MAX], r1[QH_MAX];
+  load_heads_raw<QT>(a, b, h, h0, step, lane, r0, r1);
+  load_heads_cvt<QT>(a, r0, r1, v0, v1);
 }
 
 // ------------------------------------------------------------------ retrieved role (VALU)
@@ -1077,7 +1123,7 @@ struct RetSmem {
   float lq[32 * 16 * G4];     // [channel nibble][pattern][head]: sums of q'
   float qs[G4 * D];           // rotated query heads of the segment
   float qsum[G4];
-  float xs[4][D];             // per-wave scratch of the DCT helpers
+  float xs[4][DCT_SCRATCH];   // per-wave scratch of the DCT helpers
   CombineSmem cs;
   union {
     TopkSmem tk;                // selection (before the tile loop)
@@ -1315,10 +1361,8 @@ struct RetMfmaSmem {
       int32_t sel[TOPK_MAX_K];
       u32x4 pm1[256];         // byte -> 8 fp16 values (+1 for a set bit, -1 otherwise)
       u32x4 qb[4][2][64];     // Q'^T operands per k-step and fp16 part, per lane
-      float xs[4][D];
-      struct {
-        TopkSmem tk;          // wave 0's selection scratch (while the other waves fill qb)
-      } p;
+      float xs[4][DCT_SCRATCH];
+      TopkSmem tk;            // wave 0's selection scratch (while the other waves fill qb)
     };
     float ow[4 * OW_WAVE];    // per-wave partial o' (after the tile loop)
   } u;
@@ -1338,39 +1382,35 @@ __device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
 //   O'^T[16 ch x 16 heads] += Vhat^T[16 ch x 32 tok] (sv P)^T[32 tok x 16 heads]: the
 //     S^T accumulator slots are the PV k-slots (as in the window part); Vhat^T = +-1
 //     from two nibbles of the lane's channel word; sv*P split in 2 fp16 parts.
-template <int T>
-struct MfmaTile {
-  static constexpr int W = T / 64;
-  uint64_t kw[2][W];  // K channel words of channels lane and lane + 64 (bit-transpose rows)
-  uint64_t vw[8][W];  // V channel words of channels 16 cb + n
+// One 64-token unit of a selected tile (word `half` of each channel; a T = 128 tile is
+// two units): the wave double-buffers units, not whole tiles, so its registers do not
+// grow with T.
+struct MfmaUnit {
+  uint64_t kw[2];  // K channel words of channels lane and lane + 64 (bit-transpose rows)
+  uint64_t vw[8];  // V channel words of channels 16 cb + n
   float sk, sv;
 };
 
 template <int T>
-__device__ __forceinline__ void fetch_mfma_tile(const DecodeArgs& a, int64_t seg, int64_t tile, int lane,
-                                                MfmaTile<T>& t) {
+__device__ __forceinline__ void fetch_mfma_unit(const DecodeArgs& a, int64_t seg, int64_t tile, int half,
+                                                int lane, MfmaUnit& t) {
   constexpr int W = T / 64;
   const int n = lane & 15;
   tile = tile < 0 ? 0 : (tile >= a.tile_stride ? a.tile_stride - 1 : tile);  // stay inside the store
   const int64_t slot = seg * a.tile_stride + tile;
-  const uint64_t* kp = a.kbits + slot * (int64_t)(D * W);
-  const uint64_t* vp = a.vbits + slot * (int64_t)(D * W);
+  const uint64_t* kp = a.kbits + slot * (int64_t)(D * W) + half;
+  const uint64_t* vp = a.vbits + slot * (int64_t)(D * W) + half;
+  t.kw[0] = kp[lane * W];
+  t.kw[1] = kp[(lane + 64) * W];
 #pragma unroll
-  for (int w = 0; w < W; ++w) {
-    t.kw[0][w] = kp[lane * W + w];
-    t.kw[1][w] = kp[(lane + 64) * W + w];
-  }
-#pragma unroll
-  for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-    for (int w = 0; w < W; ++w) t.vw[cb][w] = vp[(16 * cb + n) * W + w];
+  for (int cb = 0; cb < 8; ++cb) t.vw[cb] = vp[(16 * cb + n) * W];
   t.sk = f16_to_f32(a.kscale[slot]) * SCALE_LOG2;
   t.sv = f16_to_f32(a.vscale[slot]);
 }
 
-// epoch_word (fused step): the segment's epoch word; wave 0 selects from the lists of
-// this call (epoch + 1), which the segment's score items may still be writing, while the
-// other waves rotate the query heads.  Null: lists of an earlier launch.
+// epoch_word (fused step): the segment's epoch word; the selection reads the lists of
+// this call (tag epoch + 1), which the segment's score items may still be writing.
+// Null: lists of an earlier launch.
 template <int T, int QT>
 __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, RetMfmaSmem& sm, float* R,
                                     const int32_t* epoch_word = nullptr) {
@@ -1386,33 +1426,38 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int64_t b = seg / a.Hkv;
   const int64_t h = seg - b * a.Hkv;
 
-  // Wave w takes the selected tiles j = rs*4 + w, then + 4*RS, ...; the first tile's
-  // words are fetched as soon as its index is known, each next one while the current
-  // tile is processed.
+  // Wave w takes the selected tiles j = rs*4 + w, then + 4*RS, ..., as a sequence of
+  // 64-token units (tile j0 + (u / W) * jstep, word u % W); the first unit's words are
+  // fetched as soon as its index is known, each next one while the current unit is
+  // processed.
   const int jstep = 4 * a.n_rparts;
   const int j0 = rs * 4 + wv_id;
-  MfmaTile<T> cur;
+  const int n_units = (j0 < k) ? ((k - 1 - j0) / jstep + 1) * W : 0;
+  MfmaUnit cur;
   if (!a.do_select) {
-    if (j0 < k) fetch_mfma_tile<T>(a, seg, a.idx[seg * k + j0], lane, cur);
+    if (j0 < k) fetch_mfma_unit<T>(a, seg, a.idx[seg * k + j0], 0, lane, cur);
     // the tile loop reads every next index from LDS in both modes (one address space:
     // an index read through a pointer that is LDS or global would be a FLAT load)
     for (int i = tid; i < k; i += NT) sm.u.sel[i] = a.idx[seg * k + i];
   }
 
-  // wave 0 selects (when asked); waves 1..3 (or 0..3) rotate the query heads
+  // Selection (when asked): wave 0 selects, from the candidate lists or the scores,
+  // while waves 1..3 rotate the query heads.
   const int qw0 = a.do_select ? 1 : 0;
   if (a.do_select && wv_id == 0) {
     const uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
                                                                   __HIP_MEMORY_SCOPE_AGENT) + 1u
-                                   : CAND_EPOCH_CHAIN;
-    select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane, ep);
+                                   : CAND_EPOCH_CHAIN;  // the lists' tag epoch
+    select_tiles(a, seg, k, sm.u.sel, sm.u.tk, lane, ep);
     wave_lds_sync();
     if (rs == 0)
       for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.u.sel[i];
   }
   if (wv_id >= qw0) {
+    uint32_t r0[QH_MAX], r1[QH_MAX];
+    load_heads_raw<QT>(a, b, h, wv_id - qw0, 4 - qw0, lane, r0, r1);
     float v0[QH_MAX], v1[QH_MAX];
-    load_heads<QT>(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
+    load_heads_cvt<QT>(a, r0, r1, v0, v1);
 #pragma unroll
     for (int j = 0; j < QH_MAX; ++j) {
       const int hh = wv_id - qw0 + (4 - qw0) * j;
@@ -1447,22 +1492,22 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     sm.u.pm1[x] = u32x4{w[0], w[1], w[2], w[3]};
   }
   __syncthreads();
-  if (a.do_select && j0 < k) fetch_mfma_tile<T>(a, seg, sm.u.sel[j0], lane, cur);
+  const int32_t* sel = sm.u.sel;
+  if (a.do_select && j0 < k) fetch_mfma_unit<T>(a, seg, sel[j0], 0, lane, cur);
 
   f32x4 oacc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -__builtin_inff(), l_run = 0.f;
 
-  for (int j = j0; j < k; j += jstep) {
-    MfmaTile<T> nxt;  // the wave's next tile, fetched while this one is processed
-    if (j + jstep < k)
-      fetch_mfma_tile<T>(a, seg, sm.u.sel[j + jstep], lane, nxt);
+  for (int u = 0; u < n_units; ++u) {
+    MfmaUnit nxt;  // the wave's next unit, fetched while this one is processed
+    if (u + 1 < n_units)
+      fetch_mfma_unit<T>(a, seg, sel[j0 + ((u + 1) / W) * jstep], (u + 1) % W, lane, nxt);
     const float sk = cur.sk, sv = cur.sv;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      uint32_t row[4] = {(uint32_t)cur.kw[0][w], (uint32_t)(cur.kw[0][w] >> 32), (uint32_t)cur.kw[1][w],
-                         (uint32_t)(cur.kw[1][w] >> 32)};
+    {
+      uint32_t row[4] = {(uint32_t)cur.kw[0], (uint32_t)(cur.kw[0] >> 32), (uint32_t)cur.kw[1],
+                         (uint32_t)(cur.kw[1] >> 32)};
       transpose64(row[0], row[1], lane);  // lane t: token t, channels 0..63
       transpose64(row[2], row[3], lane);  // channels 64..127
 
@@ -1523,7 +1568,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
         const int sh0 = 4 * kg;
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) {
-          const uint32_t vd = (uint32_t)(cur.vw[cb][w] >> (32 * ks2));
+          const uint32_t vd = (uint32_t)(cur.vw[cb] >> (32 * ks2));
           const uint32_t lo = (vd >> sh0) & 15u;
           const uint32_t hi = (vd >> (sh0 + 16)) & 15u;
           const u32x4 av = sm.u.pm1[lo | (hi << 4)];
@@ -1606,7 +1651,7 @@ __device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, fl
 }
 
 __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
-  __shared__ float xs[D];
+  __shared__ float xs[DCT_SCRATCH];
   const int64_t bq = blockIdx.x;  // b * Hq + head
   const int64_t b = bq / a.Hq;
   const int hq = (int)(bq - b * a.Hq);
@@ -1620,7 +1665,7 @@ __global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
 // with a candidate array the item's tiles are also sorted (wave 0) into its list.
 struct ScoreSmem {
   float qs[4][D];  // per wave
-  float xs[4][D];
+  float xs[4][DCT_SCRATCH];
   uint64_t lc[128];
 };
 
@@ -1753,7 +1798,7 @@ struct StepSmem {
     WindowSmem win;
     RetMfmaSmem retm;
     ScoreSmem sc;
-    float xs[4][D];  // merge
+    float xs[4][DCT_SCRATCH];  // merge
   } u;
   int last;
 };
@@ -1828,7 +1873,7 @@ template <int QT, int TF>
 __global__ __launch_bounds__(64) void query_prep_kernel(const void* __restrict__ q, int Hq, int Hkv,
                                                         float* __restrict__ qbar_rot,
                                                         float* __restrict__ q_rot) {
-  __shared__ float xs[D];
+  __shared__ float xs[DCT_SCRATCH];
   const int lane = threadIdx.x;
   const int64_t seg = blockIdx.x;
   const int64_t b = seg / Hkv;
@@ -1946,12 +1991,17 @@ int n_window_parts(int64_t BH, int64_t win_len) {
   return (win_len > 0) ? (int)((win_len + span - 1) / span) : 0;
 }
 constexpr int RET_TILES_PER_BLOCK = KVR_RET_TILES;  // selected tiles per retrieved item
-int n_retrieved_parts(int k) { return (k > 0) ? (k + RET_TILES_PER_BLOCK - 1) / RET_TILES_PER_BLOCK : 0; }
+// Selected tiles per retrieved item: KVR_RET_TILES at T = 64, proportionally fewer at
+// T = 128 (two 64-token units per tile), so a wave walks about two units either way.
+int n_retrieved_parts(int k, int T) {
+  const int per = RET_TILES_PER_BLOCK * 64 / T >= 4 ? RET_TILES_PER_BLOCK * 64 / T : 4;
+  return (k > 0) ? (k + per - 1) / per : 0;
+}
 
 // Partial records in the workspace: one per window item and per retrieved item.
-size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k) {
+size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T) {
   const int g = Hq / Hkv;
-  const int64_t parts = n_window_parts(B * Hkv, win_len) + n_retrieved_parts(k);
+  const int64_t parts = n_window_parts(B * Hkv, win_len) + n_retrieved_parts(k, T);
   return (size_t)(B * Hkv * (parts > 0 ? parts : 1) * g * (2 + D)) * sizeof(float);
 }
 
@@ -2060,7 +2110,7 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   a.n_chunks = (int)((n_tiles + score_tiles_per_item(T) - 1) / score_tiles_per_item(T));
   a.n_wparts = n_window_parts(B * Hkv, win_len);
   a.win_span = window_span(B * Hkv, win_len);
-  a.n_rparts = n_retrieved_parts(k);
+  a.n_rparts = n_retrieved_parts(k, T);
   a.do_select = (do_select && k > 0) ? 1 : 0;
   a.cand = (a.do_select && k <= KVR_CAND_MAX && k <= 64) ? cand : nullptr;
   a.ret_method = retrieve_method();
