@@ -1362,7 +1362,11 @@ struct RetMfmaSmem {
       u32x4 pm1[256];         // byte -> 8 fp16 values (+1 for a set bit, -1 otherwise)
       u32x4 qb[4][2][64];     // Q'^T operands per k-step and fp16 part, per lane
       float xs[4][DCT_SCRATCH];
-      TopkSmem tk;            // wave 0's selection scratch (while the other waves fill qb)
+      union {
+        TopkSmem tk;          // wave 0's selection from scores (while the other waves fill qb)
+        uint64_t part[4][64]; // each wave's top 64 of its share of the candidate lists
+      } p;
+      int32_t selw[4][64];    // each wave's copy of the selection from candidate lists
     };
     float ow[4 * OW_WAVE];    // per-wave partial o' (after the tile loop)
   } u;
@@ -1441,14 +1445,19 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     for (int i = tid; i < k; i += NT) sm.u.sel[i] = a.idx[seg * k + i];
   }
 
-  // Selection (when asked): wave 0 selects, from the candidate lists or the scores,
-  // while waves 1..3 rotate the query heads.
-  const int qw0 = a.do_select ? 1 : 0;
-  if (a.do_select && wv_id == 0) {
-    const uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
-                                                                  __HIP_MEMORY_SCOPE_AGENT) + 1u
-                                   : CAND_EPOCH_CHAIN;  // the lists' tag epoch
-    select_tiles(a, seg, k, sm.u.sel, sm.u.tk, lane, ep);
+  // Selection (when asked).  From more than 8 candidate lists: every wave first rotates
+  // its query heads (the lists are usually still being written), then merges lists
+  // w, w + 4, ... into a partial top 64; the four partials meet in LDS and every wave
+  // merges them (the same result in each) into its own copy of the selection.  From
+  // fewer lists (one load batch) or the scores: wave 0 selects while waves 1..3 rotate
+  // the query heads.
+  const bool par = a.do_select && a.cand && a.n_chunks > 8;  // more than one load batch
+  const int qw0 = (a.do_select && !par) ? 1 : 0;
+  const uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT) + 1u
+                                 : CAND_EPOCH_CHAIN;  // the lists' tag epoch
+  if (a.do_select && !par && wv_id == 0) {
+    select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane, ep);
     wave_lds_sync();
     if (rs == 0)
       for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.u.sel[i];
@@ -1480,6 +1489,9 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
       }
     }
   }
+  if (par)
+    sm.u.p.part[wv_id][lane] = merge_list_set(a.cand + seg * a.n_chunks * (int64_t)128, wv_id, 4, a.n_chunks,
+                                              lane, ep, seg, a.ctr ? a.ctr + CTR_ERR_WORD : nullptr);
   {  // +-1 patterns: entry x, element e = bit e of x
     const int x = tid;
     uint32_t w[4];
@@ -1493,6 +1505,15 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   }
   __syncthreads();
   const int32_t* sel = sm.u.sel;
+  if (par) {
+    uint64_t acc = sm.u.p.part[0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) acc = merge_top64(acc, sm.u.p.part[w][63 - lane], lane);
+    sm.u.selw[wv_id][lane] = (int32_t)cand_tile(acc);
+    wave_lds_sync();
+    if (wv_id == 0 && rs == 0 && lane < k) a.idx[seg * k + lane] = (int32_t)cand_tile(acc);
+    sel = sm.u.selw[wv_id];
+  }
   if (a.do_select && j0 < k) fetch_mfma_unit<T>(a, seg, sel[j0], 0, lane, cur);
 
   f32x4 oacc[8];
@@ -1592,37 +1613,39 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
 
 // ------------------------------------------------------------------ merge
 
+__device__ __forceinline__ float2 rec_load2(const float* p) {  // 8-byte aligned
+  return __builtin_bit_cast(float2, __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+
 // One wave per (sequence, query head i of segment seg): LSE-merge every partial record
 // of the segment (window parts in the original domain, retrieved parts rotated; their
-// sum is rotated back once), normalise, store.  Record loads are clamped and
-// branch-free so a batch of parts is in flight together.
-__device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, float* xs) {
-  constexpr int MAXP = 16;  // records loaded per batch
+// sum is rotated back once), normalise, store.  Parts go in batches of MAXP, every load
+// of a batch in flight together: lane p loads part p's max and sum, every lane the
+// part's two output channels; the batch max and the sum of l * exp2(m - max) are wave
+// reductions, the per-part weights are read from their lanes.  The order of every sum
+// is fixed, so the result is deterministic.
+template <int MAXP>
+__device__ __forceinline__ void merge_parts(const DecodeArgs& a, const float* R0, int64_t rs, int i, int lane,
+                                            float& M, float& L, float& w0, float& w1, float& r0, float& r1) {
   const int g = a.g;
-  const int64_t bq = (seg / a.Hkv) * a.Hq + (seg % a.Hkv) * g + i;  // b * Hq + head
   const int n_parts = a.n_wparts + a.n_rparts;
-  const int64_t rs = g * (2 + D);
-  const float* R0 = a.rec + seg * n_parts * rs;
-
-  float M = -__builtin_inff(), L = 0.f, w0 = 0.f, w1 = 0.f, r0 = 0.f, r1 = 0.f;
   for (int p0 = 0; p0 < n_parts; p0 += MAXP) {
-    float pm[MAXP], pl[MAXP];
+    const bool mine = lane < MAXP && p0 + lane < n_parts;  // this lane's part of the batch
+    const float* Rl = R0 + (mine ? p0 + lane : p0) * rs;
+    const float pm = rec_load(Rl + i);
+    const float pl = rec_load(Rl + g + i);
     float2 po[MAXP];
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
       const int pc = (p0 + p < n_parts) ? p0 + p : n_parts - 1;
-      const float* R = R0 + pc * rs;
-      pm[p] = rec_load(R + i);
-      pl[p] = rec_load(R + g + i);
-      po[p] = make_float2(rec_load(R + 2 * g + i * D + 2 * lane), rec_load(R + 2 * g + i * D + 2 * lane + 1));
+      po[p] = rec_load2(R0 + pc * rs + 2 * g + i * D + 2 * lane);
     }
-    float Mb = -__builtin_inff();
-#pragma unroll
-    for (int p = 0; p < MAXP; ++p) Mb = fmaxf(Mb, pm[p]);
-    const float Mn = fmaxf(M, Mb);
+    const float Mn = fmaxf(M, wave_max(mine ? pm : -__builtin_inff()));
     const float mu = (Mn == -__builtin_inff()) ? 0.f : Mn;
     const float sc = fast_exp2(M - mu);
-    L *= sc;
+    const float f = mine ? fast_exp2(pm - mu) : 0.f;
+    L = L * sc + wave_sum(pl * f);
     w0 *= sc;
     w1 *= sc;
     r0 *= sc;
@@ -1630,15 +1653,37 @@ __device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, fl
     M = Mn;
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
-      const float f = (p0 + p < n_parts) ? fast_exp2(pm[p] - mu) : 0.f;
-      const bool win = p0 + p < a.n_wparts;
-      L += pl[p] * f;
-      w0 += win ? po[p].x * f : 0.f;
-      w1 += win ? po[p].y * f : 0.f;
-      r0 += win ? 0.f : po[p].x * f;
-      r1 += win ? 0.f : po[p].y * f;
+      const float fp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), p));  // 0 past the end
+      if (p0 + p < a.n_wparts) {
+        w0 = fmaf(po[p].x, fp, w0);
+        w1 = fmaf(po[p].y, fp, w1);
+      } else {
+        r0 = fmaf(po[p].x, fp, r0);
+        r1 = fmaf(po[p].y, fp, r1);
+      }
     }
   }
+}
+
+// Sums of head i over the segment's parts on one wave (channels 2 lane, 2 lane + 1):
+// L, the window part w and the (rotated) retrieved part r, all scaled to one max.
+__device__ __forceinline__ void merge_sums(const DecodeArgs& a, int64_t seg, int i, int lane, float& L, float& w0,
+                                           float& w1, float& r0, float& r1) {
+  const int n_parts = a.n_wparts + a.n_rparts;
+  const int64_t rs = a.g * (2 + D);
+  const float* R0 = a.rec + seg * n_parts * rs;
+  // batches of 8, 16 or 32 parts: no more loads than parts for small segments
+  float M = -__builtin_inff();
+  L = w0 = w1 = r0 = r1 = 0.f;
+  if (n_parts <= 8) merge_parts<8>(a, R0, rs, i, lane, M, L, w0, w1, r0, r1);
+  else if (n_parts <= 16) merge_parts<16>(a, R0, rs, i, lane, M, L, w0, w1, r0, r1);
+  else merge_parts<32>(a, R0, rs, i, lane, M, L, w0, w1, r0, r1);
+}
+
+__device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, float* xs) {
+  const int64_t bq = (seg / a.Hkv) * a.Hq + (seg % a.Hkv) * a.g + i;  // b * Hq + head
+  float L, w0, w1, r0, r1;
+  merge_sums(a, seg, i, lane, L, w0, w1, r0, r1);
   if (a.n_rparts > 0) unrotate_pair(r0, r1, lane, a.transform, xs);
   const float inv = (L > 0.f) ? 1.f / L : 0.f;
   const float y0 = (w0 + r0) * inv, y1 = (w1 + r1) * inv;
@@ -1647,6 +1692,70 @@ __device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, fl
     ((float2*)a.out)[o >> 1] = make_float2(y0, y1);
   } else {
     ((uint32_t*)a.out)[o >> 1] = pack2(f32_to_bf16_rne(y0), f32_to_bf16_rne(y1));
+  }
+}
+
+// Whole-segment merge for DCT segments with retrieved parts, on the block's four waves.
+// Phase A: every head's sums (one wave per head) into LDS as [channel][head] columns.
+// Phase B: the retrieved sums of all heads are rotated back at once on MFMA, wave w
+// taking output channels [32 w, 32 w + 32): out[n][h] = (W[n][h] + sum_k C[k][n] R[k][h])
+// / L[h], as 16x16x4 fp32 products (C^T rows from the matrix in constant memory, loaded
+// before phase A so they arrive meanwhile).  Head columns past g are not stored.
+struct MergeSmem {
+  float rt[D][17];  // retrieved sums [channel][head] (row padded: conflict-free columns)
+  float wt[D][17];  // window sums
+  float inv[16];    // 1 / L per head
+};
+
+__device__ __forceinline__ f32x4 mfma16_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ void merge_segment_rot(const DecodeArgs& a, int64_t seg, MergeSmem& ms) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int g = a.g;
+  const int hc = lane & 15;  // head column (B and D operands), row of A
+  const int kq = lane >> 4;  // k within a step (A and B), row group of D
+  // A[m][kk] = C^T[32 w + 16 mb + m][4 ks + kk] = C[4 ks + kk][32 w + 16 mb + m]
+  float av[2][32];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int ks = 0; ks < 32; ++ks) av[mb][ks] = g_dct[(4 * ks + kq) * D + 32 * w + 16 * mb + hc];
+
+  for (int hh = w; hh < g; hh += 4) {
+    float L, w0, w1, r0, r1;
+    merge_sums(a, seg, hh, lane, L, w0, w1, r0, r1);
+    ms.rt[2 * lane][hh] = r0;
+    ms.rt[2 * lane + 1][hh] = r1;
+    ms.wt[2 * lane][hh] = w0;
+    ms.wt[2 * lane + 1][hh] = w1;
+    if (lane == 0) ms.inv[hh] = (L > 0.f) ? 1.f / L : 0.f;
+  }
+  __syncthreads();
+
+  float bv[32];  // B[kk][h] = R[4 ks + kk][h]
+#pragma unroll
+  for (int ks = 0; ks < 32; ++ks) bv[ks] = ms.rt[4 * ks + kq][hc];
+  const float inv = hc < g ? ms.inv[hc] : 0.f;
+  const int64_t bq = (seg / a.Hkv) * a.Hq + (seg % a.Hkv) * g + hc;  // b * Hq + head
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    const int n0 = 32 * w + 16 * mb + 4 * kq;  // D rows n0 .. n0 + 3 of head column hc
+    f32x4 acc = f32x4{ms.wt[n0][hc], ms.wt[n0 + 1][hc], ms.wt[n0 + 2][hc], ms.wt[n0 + 3][hc]};
+#pragma unroll
+    for (int ks = 0; ks < 32; ++ks) acc = mfma16_f32(av[mb][ks], bv[ks], acc);
+    if (hc < g) {
+      const int64_t o = bq * D + n0;
+      if (a.out_dtype == KVR_FP32) {
+        *(float4*)((float*)a.out + o) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+      } else {
+        *(uint2*)((uint16_t*)a.out + o) = make_uint2(pack2(f32_to_bf16_rne(acc[0] * inv), f32_to_bf16_rne(acc[1] * inv)),
+                                                     pack2(f32_to_bf16_rne(acc[2] * inv), f32_to_bf16_rne(acc[3] * inv)));
+      }
+    }
   }
 }
 
@@ -1798,7 +1907,8 @@ struct StepSmem {
     WindowSmem win;
     RetMfmaSmem retm;
     ScoreSmem sc;
-    float xs[4][DCT_SCRATCH];  // merge
+    float xs[4][DCT_SCRATCH];  // merge, one head per wave
+    MergeSmem mg;              // merge, DCT segments
   } u;
   int last;
 };
@@ -1852,7 +1962,9 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a
       ctr_store(rdone + seg * CTR_STRIDE, 0);
     }
     const int w = tid >> 6;
-    for (int hh = w; hh < a.g; hh += 4) merge_head(a, seg, hh, tid & 63, sm.u.xs[w]);
+    if (a.transform == KVR_DCT && a.n_rparts > 0) merge_segment_rot(a, seg, sm.u.mg);
+    else
+      for (int hh = w; hh < a.g; hh += 4) merge_head(a, seg, hh, tid & 63, sm.u.xs[w]);
   }
 }
 
