@@ -220,22 +220,31 @@ static __constant__ CosTable g_cos_tab = make_cos_table();
 // Floats of a wave's LDS scratch for dct_pair / idct_pair: the vector, then the table.
 constexpr int DCT_SCRATCH = D + 516;
 
-__device__ __forceinline__ void dct_table_to_lds(float* cs, int lane) {
+// The table is staged by each wave that uses it, at xs + D of its scratch: loaded into
+// registers first (dct_table_load, issued early so that its latency overlaps other
+// loads), then stored (dct_table_store) before the wave's first DCT.
+struct DctRegs {
+  float4 t0, t1, t2;
+};
+__device__ __forceinline__ DctRegs dct_table_load(int lane) {
   const float4* src = (const float4*)g_cos_tab.v;
-  const float4 t0 = src[lane], t1 = src[lane + 64];
-  ((float4*)cs)[lane] = t0;
-  ((float4*)cs)[lane + 64] = t1;
-  if (lane == 0) ((float4*)cs)[128] = src[128];
+  return DctRegs{src[lane], src[lane + 64], src[128]};
 }
+__device__ __forceinline__ void dct_table_store(const DctRegs& r, float* xs, int lane) {
+  float4* cs = (float4*)(xs + D);
+  cs[lane] = r.t0;
+  cs[lane + 64] = r.t1;
+  if (lane == 0) cs[128] = r.t2;
+}
+__device__ __forceinline__ void dct_table_to_lds(float* xs, int lane) { dct_table_store(dct_table_load(lane), xs, lane); }
 
 // y = C x for a vector held as channels (2*lane, 2*lane+1), through the caller's
-// wave-private LDS scratch xs[DCT_SCRATCH].  C[k][127-n] = (-1)^k C[k][n], so with
+// wave-private LDS scratch xs[DCT_SCRATCH] (the table staged at xs + D).  C[k][127-n] = (-1)^k C[k][n], so with
 // s[n] = x[n] + x[127-n] and d[n] = x[n] - x[127-n] (n < 64) an even row is
 // sum_n C[k][n] s[n] and an odd row sum_n C[k][n] d[n]: 64 LDS table reads per output.
 // Tolerance path (fmaf, a different summation order than the plain product).
 __device__ __forceinline__ void dct_pair(float& v0, float& v1, int lane, float* xs) {
-  float* cs = xs + D;
-  dct_table_to_lds(cs, lane);
+  const float* cs = xs + D;
   xs[2 * lane] = v0;
   xs[2 * lane + 1] = v1;
   __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -264,12 +273,11 @@ __device__ __forceinline__ void dct_pair(float& v0, float& v1, int lane, float* 
   v1 = a1;
 }
 
-// x = C^T y for a vector held as channels (2*lane, 2*lane+1): lane n < 64 sums the even
-// rows E = sum C[2j][n] y[2j] and the odd rows O = sum C[2j+1][n] y[2j+1]; then
-// x[n] = E + O and x[127-n] = E - O.
+// x = C^T y for a vector held as channels (2*lane, 2*lane+1) (the table staged at
+// xs + D): lane n < 64 sums the even rows E = sum C[2j][n] y[2j] and the odd rows
+// O = sum C[2j+1][n] y[2j+1]; then x[n] = E + O and x[127-n] = E - O.
 __device__ __forceinline__ void idct_pair(float& v0, float& v1, int lane, float* xs) {
-  float* cs = xs + D;
-  dct_table_to_lds(cs, lane);
+  const float* cs = xs + D;
   xs[2 * lane] = v0;
   xs[2 * lane + 1] = v1;
   __builtin_amdgcn_s_waitcnt(0xc07f);

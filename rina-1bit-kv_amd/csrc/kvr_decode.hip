@@ -62,7 +62,10 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #define KVR_STEP_ORDER 1
 #endif
 #ifndef KVR_SCORE_TPG
-#define KVR_SCORE_TPG 6  // tiles per 16-lane group of a score item at T = 64 (half at T = 128): 4, 6 or 8
+#define KVR_SCORE_TPG 6  // tiles per 16-lane group of a score item at T = 64: 4, 6 or 8
+#endif
+#ifndef KVR_SCORE_TPG128  // the same at T = 128 (two words per channel)
+#define KVR_SCORE_TPG128 2
 #endif
 #ifndef KVR_CTR_STRIDE
 #define KVR_CTR_STRIDE 32  // int32 words between per-segment counters (32: a 128-byte line each)
@@ -245,7 +248,7 @@ __device__ __forceinline__ void qbar_load(const DecodeArgs& a, int64_t seg, int 
 
 template <int QT>
 __device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, uint32_t* r1, float* qs, float* xs,
-                                            int lane) {
+                                            int lane, const DctRegs& dt) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     pin(r0[i]);
@@ -264,6 +267,7 @@ __device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, u
   }
   m0 = __fdiv_rn(m0, (float)a.g);
   m1 = __fdiv_rn(m1, (float)a.g);
+  if (a.transform == KVR_DCT) dct_table_store(dt, xs, lane);
   rotate_pair(m0, m1, lane, a.transform, xs);
   qs[2 * lane] = m0;
   qs[2 * lane + 1] = m1;
@@ -272,7 +276,9 @@ __device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, u
 __device__ void qbar_wave(const DecodeArgs& a, int64_t seg, float* qs, float* xs, int lane) {
   uint32_t r0[16], r1[16];
   qbar_load<Q_RUNTIME>(a, seg, lane, r0, r1);
-  qbar_finish<Q_RUNTIME>(a, r0, r1, qs, xs, lane);
+  DctRegs dt{};
+  if (a.transform == KVR_DCT) dt = dct_table_load(lane);
+  qbar_finish<Q_RUNTIME>(a, r0, r1, qs, xs, lane, dt);
 }
 
 // Selection candidate (score_key << 32) | (0xffffffff - tile): a larger value is a
@@ -307,17 +313,19 @@ __device__ __forceinline__ float tree16(float p) {
 }
 
 // Score items: 16 lanes per tile, lane li owns channels 8li..8li+7; each 16-lane group
-// scores TPG tiles (16 * KVR_SCORE_TPG words in flight per lane for either T), so an
-// item covers 16*TPG tiles.  The words are loaded before the query is ready (one HBM
+// scores TPG tiles (16 * TPG * T / 64 words in flight per lane), so an item covers
+// 16*TPG tiles.  The words are loaded before the query is ready (one HBM
 // round trip per item, overlapped with the query prologue).
+constexpr int score_tpg(int T) { return T == 64 ? KVR_SCORE_TPG : KVR_SCORE_TPG128; }
+
 template <int T>
 struct ScoreWords {
   static constexpr int W = T / 64;
-  static constexpr int TPG = KVR_SCORE_TPG / W;
+  static constexpr int TPG = score_tpg(T);
   uint64_t w[TPG][8 * W];
 };
 
-constexpr int score_tiles_per_item(int T) { return 16 * (KVR_SCORE_TPG / (T / 64)); }
+constexpr int score_tiles_per_item(int T) { return 16 * score_tpg(T); }
 // Candidate slots of a score item (its tiles, padded to a multiple of 64).
 constexpr int score_cand_slots(int T) { return score_tiles_per_item(T) <= 64 ? 64 : 128; }
 
@@ -1190,8 +1198,11 @@ __device__ __forceinline__ void retrieved_role(const DecodeArgs& a, int64_t seg,
       for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.sel[i];
   }
   if (wv_id >= qw0) {
+    DctRegs dt{};
+    if (a.transform == KVR_DCT) dt = dct_table_load(lane);
     float v0[QH_MAX], v1[QH_MAX];
     load_heads<QT>(a, b, h, wv_id - qw0, 4 - qw0, lane, v0, v1);
+    if (a.transform == KVR_DCT) dct_table_store(dt, sm.xs[wv_id], lane);
 #pragma unroll
     for (int j = 0; j < QH_MAX; ++j) {
       const int hh = wv_id - qw0 + (4 - qw0) * j;
@@ -1465,8 +1476,11 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   if (wv_id >= qw0) {
     uint32_t r0[QH_MAX], r1[QH_MAX];
     load_heads_raw<QT>(a, b, h, wv_id - qw0, 4 - qw0, lane, r0, r1);
+    DctRegs dt{};
+    if (a.transform == KVR_DCT) dt = dct_table_load(lane);  // in flight with the query loads
     float v0[QH_MAX], v1[QH_MAX];
     load_heads_cvt<QT>(a, r0, r1, v0, v1);
+    if (a.transform == KVR_DCT) dct_table_store(dt, sm.u.xs[wv_id], lane);
 #pragma unroll
     for (int j = 0; j < QH_MAX; ++j) {
       const int hh = wv_id - qw0 + (4 - qw0) * j;
@@ -1682,8 +1696,12 @@ __device__ __forceinline__ void merge_sums(const DecodeArgs& a, int64_t seg, int
 
 __device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, float* xs) {
   const int64_t bq = (seg / a.Hkv) * a.Hq + (seg % a.Hkv) * a.g + i;  // b * Hq + head
+  const bool dct = a.transform == KVR_DCT && a.n_rparts > 0;
+  DctRegs dt{};
+  if (dct) dt = dct_table_load(lane);
   float L, w0, w1, r0, r1;
   merge_sums(a, seg, i, lane, L, w0, w1, r0, r1);
+  if (dct) dct_table_store(dt, xs, lane);
   if (a.n_rparts > 0) unrotate_pair(r0, r1, lane, a.transform, xs);
   const float inv = (L > 0.f) ? 1.f / L : 0.f;
   const float y0 = (w0 + r0) * inv, y1 = (w1 + r1) * inv;
@@ -1800,9 +1818,11 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int 
   const bool helper = wv == helper_wave;
   uint32_t qv0[16], qv1[16];
   qbar_load<QT>(a, seg, lane, qv0, qv1);
+  DctRegs dt{};
+  if (a.transform == KVR_DCT) dt = dct_table_load(lane);  // before the words: no wait on them
   ScoreWords<T> sw;
   score_load<T>(a.kbits, seg, a.tile_stride, t0, t1, sw);
-  qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane);
+  qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane, dt);
   wave_lds_sync();
   score_compute<T, 0>(sm.qs[wv], sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
   if (a.cand) {
@@ -1988,6 +2008,7 @@ __global__ __launch_bounds__(64) void query_prep_kernel(const void* __restrict__
   __shared__ float xs[DCT_SCRATCH];
   const int lane = threadIdx.x;
   const int64_t seg = blockIdx.x;
+  if (TF == KVR_DCT) dct_table_to_lds(xs, lane);
   const int64_t b = seg / Hkv;
   const int h = (int)(seg - b * Hkv);
   const int g = Hq / Hkv;
