@@ -211,6 +211,59 @@ def encode_benchmark(steps):
             "encode_ms": round(ms, 4), "encode_bytes": nbytes, "encode_gbps": round(nbytes / ms / 1e6, 1)}
 
 
+def e2e_benchmark(n_prompt=65536, n_new=128, n_layers=32):
+    """end-to-end greedy decode with KVRGenerator (window 2048, top-64 tiles of 64,
+    Hadamard) on a random-init Llama-3-8B-architecture model in bf16 (32 layers, d_model 4096,
+    32/8 heads, FFN 14336, vocab 128256, RoPE base 500000), batch 1, after a prompt of
+    uniform random token ids (seed 0).  The prompt goes through the model once (SDPA attention;
+    the materialising math backend is switched off so a 64 k prompt never builds N x N scores)
+    with every layer's K/V encoded as it is produced; then n_new greedy steps, timed with events
+    as one async sequence (the generated ids stay on the device)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from modules import KVRGenerator
+    torch.backends.cuda.enable_math_sdp(False)
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=n_layers,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                      max_position_embeddings=n_prompt + n_new + 64, rope_theta=500000.0,
+                      attn_implementation="sdpa")
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("cuda"):
+            model = LlamaForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    ids = torch.randint(0, cfg.vocab_size, (1, n_prompt), generator=torch.Generator().manual_seed(0)).cuda()
+    gen = KVRGenerator(model, window_size=2048, top_k=64 * 64)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    gen.prefill(ids)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log(f"  e2e prefill of {n_prompt} tokens: {prefill_s:.2f} s")
+    gen.step(ids[:, -1:], do_sample=False)  # step 0 (its token is already stored), untimed
+    for _ in range(2):
+        gen.step(do_sample=False)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n_new):
+        gen.step(do_sample=False)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    res = {"e2e_config": f"configs[3]: random-init Llama-3-8B architecture ({n_layers} layers), bf16, batch 1, "
+                         f"{n_prompt}-token random prompt, window 2048, top-64 tiles of 64",
+           "e2e_prefill_s": round(prefill_s, 3), "e2e_new_tokens": n_new,
+           "e2e_decode_ms_per_token": round(ms / n_new, 4),
+           "e2e_decode_tokens_per_s": round(n_new / (ms / 1e3), 2),
+           "e2e_context_at_end": gen.kvr._context_len}
+    del gen, model
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(wl, min_seconds=12.0):
     """The numpy oracle on one host core, repeating the whole-batch decode step (query prep,
     scoring of every tile, top-k, float64 attention; all B sequences) until min_seconds of
@@ -274,6 +327,10 @@ def main():
     ap.add_argument("--no-rotate", action="store_true", help="skip the rotating-layers (HBM-resident) leg")
     ap.add_argument("--no-cfg4", action="store_true", help="skip the configs[4] (DCT, T=128) decode leg")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--e2e", action="store_true", help="also run the configs[3] end-to-end decode leg")
+    ap.add_argument("--e2e-prompt", type=int, default=65536)
+    ap.add_argument("--e2e-new", type=int, default=128)
+    ap.add_argument("--e2e-layers", type=int, default=32)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -328,6 +385,11 @@ def main():
     enc = {} if args.no_encode else encode_benchmark(10)
     if enc:
         log(f"  encode configs[1]: {enc['encode_ms']:.3f} ms, {enc['encode_gbps']} GB/s")
+    e2e = {}
+    if args.e2e:
+        log(f"configs[3] end-to-end: {args.e2e_layers} layers, prompt {args.e2e_prompt}, {args.e2e_new} new tokens ...")
+        e2e = e2e_benchmark(args.e2e_prompt, args.e2e_new, args.e2e_layers)
+        log(f"  e2e decode: {e2e['e2e_decode_tokens_per_s']} tokens/s ({e2e['e2e_decode_ms_per_token']} ms/token)")
     cpu = None if args.no_cpu else cpu_baseline(wl)
     if cpu:
         log(f"  cpu baseline: {cpu['value']} tokens/s ({cpu['sample']})")
@@ -360,7 +422,7 @@ def main():
                   "tokens_per_s_32_layers": round(wl.B / (ms / 1e3) / 32, 1),
                   "window_mfma_tflops": round(wl.window_flops() / ms / 1e9, 2),
                   "window_mfma_util_vs_bf16_dense": round(wl.window_flops() / ms / 1e9 / BF16_DENSE_TFLOPS, 5),
-                  **cfg4,
+                  **cfg4, **e2e,
                   "rotating_4_layers_us_per_step": round(cold_ms * 1e3, 2) if cold_ms else None,
                   "rotating_4_layers_gbps": round(total / cold_ms / 1e6, 1) if cold_ms else None, **enc,
                   **{k: round(v, 5) for k, v in breakdown.items()}},
