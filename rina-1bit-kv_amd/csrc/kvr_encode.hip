@@ -145,6 +145,129 @@ __global__ __launch_bounds__(64) void encode_tiles_kernel(
   if (lane == 0) scales[slot] = (uint16_t)s16;
 }
 
+// T = 64 with a Hadamard or no rotation: the same codec with half the LDS.  Phase A
+// (lane = token) rotates the token in registers; its channels 0..63 go through the LDS
+// transpose first, and lane c keeps channel c's 64 values in registers (with the first
+// half of its |y| sum) while channels 64..127 take the same LDS rows.  The scale's sum
+// order is the codec's (per channel sequential over tokens, then j += j + 64 and the
+// lane tree), and so is the sigma-delta.  A 16.6 KB transpose lets about nine waves
+// share a CU (the full-tile kernel's 33 KB allows four), so one wave's loads run
+// while others rotate and quantise.
+template <int DT, int TF>
+__global__ __launch_bounds__(64) void encode_tiles64_kernel(
+    const void* __restrict__ x, int64_t n_h, int64_t n_tiles, int64_t n_tok, int64_t stride_b,
+    int64_t stride_h, int64_t stride_t, uint64_t* __restrict__ bits, uint16_t* __restrict__ scales,
+    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg) {
+  static_assert(TF != KVR_DCT, "the DCT rotation uses the full-tile kernel");
+  constexpr int T = 64;
+  constexpr int H = D / 2;     // channels per transpose half
+  constexpr int LDW = T + 1;  // padded row: conflict-free column writes and row reads
+  __shared__ float ys[H * LDW];
+
+  const int lane = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int64_t seg = blk / n_tiles;
+  const int64_t tile = blk - seg * n_tiles;
+  const int64_t b = seg / n_h;
+  const int64_t h = seg - b * n_h;
+
+  // ---------------- phase A: lane = token
+  const int64_t tok = tile * T + lane;
+  const int64_t base = b * stride_b + h * stride_h + tok * stride_t;
+  float v[D];
+  if constexpr (DT == KVR_FP32) {
+    const float4* src = (const float4*)((const float*)x + base);
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) {
+      float4 f = src[i];
+      v[4 * i] = f.x;
+      v[4 * i + 1] = f.y;
+      v[4 * i + 2] = f.z;
+      v[4 * i + 3] = f.w;
+    }
+  } else {
+    const uint4* src = (const uint4*)((const uint16_t*)x + base);
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+      uint4 r = src[i];
+      uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == KVR_BF16) {
+          v[8 * i + 2 * k] = __uint_as_float(w4[k] << 16);
+          v[8 * i + 2 * k + 1] = __uint_as_float(w4[k] & 0xffff0000u);
+        } else {
+          v[8 * i + 2 * k] = f16_to_f32(w4[k] & 0xffffu);
+          v[8 * i + 2 * k + 1] = f16_to_f32(w4[k] >> 16);
+        }
+      }
+    }
+  }
+  if constexpr (TF == KVR_HADAMARD) {
+    fwht128_regs(v);
+#pragma unroll
+    for (int j = 0; j < D; ++j) v[j] = v[j] * C_HAD;
+  }
+  if (dbg) {
+    float4* d4 = (float4*)(dbg + (seg * n_tok + tok) * D);
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) d4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  }
+
+  // ---------------- channels 0..63: lane c keeps channel c in registers
+#pragma unroll
+  for (int j = 0; j < H; ++j) ys[j * LDW + lane] = v[j];
+  __syncthreads();
+  const float* yr = ys + lane * LDW;
+  float y0[T];
+  float s0 = 0.f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    y0[t] = yr[t];
+    s0 = s0 + fabsf(y0[t]);
+  }
+  __syncthreads();
+  // ---------------- channels 64..127 through the same rows
+#pragma unroll
+  for (int j = 0; j < H; ++j) ys[j * LDW + lane] = v[H + j];
+  __syncthreads();
+  float s1 = 0.f;
+#pragma unroll 8
+  for (int t = 0; t < T; ++t) s1 = s1 + fabsf(yr[t]);
+
+  float a = s0 + s1;  // tree step j += j + 64
+  a = a + xor_lane_f<32>(a);
+  a = a + xor_lane_f<16>(a);
+  a = a + xor_lane_f<8>(a);
+  a = a + xor_lane_f<4>(a);
+  a = a + xor_lane_f<2>(a);
+  a = a + xor_lane_f<1>(a);
+  float mean = a * (1.0f / (float)(T * D));
+  mean = (mean < FP16_MAX) ? mean : FP16_MAX;
+  const uint32_t s16 = f32_to_f16_rne(mean);
+  const float s32 = f16_to_f32(s16);
+
+  uint32_t w0[2] = {0u, 0u}, w1[2] = {0u, 0u};
+  float e0 = 0.f, e1 = 0.f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    float u0 = y0[t] + e0;
+    float u1 = yr[t] + e1;
+    bool b0 = u0 >= 0.f;
+    bool b1 = u1 >= 0.f;
+    e0 = u0 - (b0 ? s32 : -s32);
+    e1 = u1 - (b1 ? s32 : -s32);
+    w0[t >> 5] |= (uint32_t)b0 << (t & 31);
+    w1[t >> 5] |= (uint32_t)b1 << (t & 31);
+  }
+
+  const int64_t slot = seg * out_tile_stride + out_tile_offset + tile;
+  uint64_t* out = bits + slot * (int64_t)D;
+  out[lane] = ((uint64_t)w0[1] << 32) | w0[0];
+  out[lane + 64] = ((uint64_t)w1[1] << 32) | w1[0];
+  if (lane == 0) scales[slot] = (uint16_t)s16;
+}
+
 template <int DT, int TF>
 static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h, int64_t n_tok,
                                   int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
@@ -154,7 +277,10 @@ static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h
   const int64_t nblk = n_b * n_h * n_tiles;
   if (nblk == 0) return hipSuccess;
   dim3 grid((unsigned)nblk), block(64);
-  if (T == 64)
+  if (T == 64 && TF != KVR_DCT)
+    hipLaunchKernelGGL((encode_tiles64_kernel<DT, TF == KVR_DCT ? KVR_NONE : TF>), grid, block, 0, s, x,
+                       n_h, n_tiles, n_tok, sb, sh, st, bits, scales, ots, oto, dbg);
+  else if (T == 64)
     hipLaunchKernelGGL((encode_tiles_kernel<DT, TF, 64>), grid, block, 0, s, x, n_h, n_tiles, n_tok,
                        sb, sh, st, bits, scales, ots, oto, dbg);
   else
