@@ -268,6 +268,149 @@ __global__ __launch_bounds__(64) void encode_tiles64_kernel(
   if (lane == 0) scales[slot] = (uint16_t)s16;
 }
 
+// DCT-II rotation of bf16 input on MFMA, then the same scale and sigma-delta.  Per tile,
+// Y[token][out] = sum_in X[token][in] C[out][in] as v_mfma_f32_16x16x32_bf16 products:
+// the input is exact in bf16, and C is split into three bf16 parts (c1 + c2 + c3 carries
+// C's fp32 value to about 2^-27 relative), so every product is exact in fp32 and the
+// rotation matches C x to fp32 accumulation error (the DCT rotation is held to a
+// tolerance; the codec is exact given the rotation the kernel wrote).  Four waves per
+// block: wave w owns output channels [32 w, 32 w + 32) and keeps their C operands in
+// registers; blocks are persistent over tiles so the split is done once per block.
+// Phase A writes Y to LDS as [channel][token]; phase B: threads 0..127 take channel
+// tid (per-channel sequential |y| sum, the codec's j += j + 64 then lane tree, then
+// the sigma-delta recurrence and the channel's words).
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+constexpr int DCT_ENC_BLOCKS = 512;  // persistent blocks (two per CU: 66 KB of LDS each at T = 128)
+
+template <int T>
+__global__ __launch_bounds__(256, 2) void encode_dct_mfma_kernel(
+    const uint16_t* __restrict__ x, int64_t n_h, int64_t n_tiles, int64_t n_tok, int64_t stride_b,
+    int64_t stride_h, int64_t stride_t, uint64_t* __restrict__ bits, uint16_t* __restrict__ scales,
+    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg, int64_t n_blk) {
+  constexpr int LDW = T + 1;  // padded row
+  constexpr int W = T / 64;
+  constexpr int NBC = 4;      // 16-token blocks per load batch
+  __shared__ float ys[D * LDW];
+  __shared__ float ssum[D];
+  __shared__ float sbc;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int n = lane & 15;   // token row of A, output column of B and D
+  const int kg = lane >> 4;  // k group (8 inputs) of A and B, row group of D
+
+  // B operands: C^T[in 32 ks + 8 kg + e][out 32 wv + 16 mb + n] in three bf16 parts
+  u32x4 cb[2][4][3];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint32_t hp[3][8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float r = g_dct[(32 * wv + 16 * mb + n) * D + 32 * ks + 8 * kg + e];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          const uint32_t hb = f32_to_bf16_rne(r);
+          hp[p][e] = hb;
+          r = r - __uint_as_float(hb << 16);  // exact: r and its bf16 rounding are close
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        cb[mb][ks][p] = u32x4{hp[p][0] | (hp[p][1] << 16), hp[p][2] | (hp[p][3] << 16),
+                              hp[p][4] | (hp[p][5] << 16), hp[p][6] | (hp[p][7] << 16)};
+    }
+
+  for (int64_t blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
+    const int64_t seg = blk / n_tiles;
+    const int64_t tile = blk - seg * n_tiles;
+    const int64_t b = seg / n_h;
+    const int64_t h = seg - b * n_h;
+    const uint16_t* xs = x + b * stride_b + h * stride_h;
+
+    // ---------------- phase A: Y = X C^T into ys[out][token]
+#pragma unroll
+    for (int nb0 = 0; nb0 < T / 16; nb0 += NBC) {
+      u32x4 xa[NBC][4];  // A operands: token 16 nb + n, inputs 32 ks + 8 kg .. + 7
+#pragma unroll
+      for (int j = 0; j < NBC; ++j) {
+        const uint16_t* xr = xs + (tile * T + 16 * (nb0 + j) + n) * stride_t + 8 * kg;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) xa[j][ks] = *(const u32x4*)(xr + 32 * ks);
+      }
+#pragma unroll
+      for (int j = 0; j < NBC; ++j)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int p = 0; p < 3; ++p) acc = mfma_bf16(xa[j][ks], cb[mb][ks][p], acc);
+          // acc[r] = Y[token 16 nb + 4 kg + r][out 32 wv + 16 mb + n]
+          const int ch = 32 * wv + 16 * mb + n;
+          const int t0 = 16 * (nb0 + j) + 4 * kg;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ys[ch * LDW + t0 + r] = acc[r];
+          if (dbg) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dbg[(seg * n_tok + tile * T + t0 + r) * D + ch] = acc[r];
+          }
+        }
+    }
+    __syncthreads();
+
+    // ---------------- phase B: thread c < 128 takes channel c
+    const float* yr = ys + tid * LDW;
+    if (tid < D) {
+      float sa = 0.f;
+#pragma unroll 8
+      for (int t = 0; t < T; ++t) sa = sa + fabsf(yr[t]);
+      ssum[tid] = sa;
+    }
+    __syncthreads();
+    if (wv == 0) {
+      float a = ssum[lane] + ssum[lane + 64];  // tree step j += j + 64
+      a = a + xor_lane_f<32>(a);
+      a = a + xor_lane_f<16>(a);
+      a = a + xor_lane_f<8>(a);
+      a = a + xor_lane_f<4>(a);
+      a = a + xor_lane_f<2>(a);
+      a = a + xor_lane_f<1>(a);
+      float mean = a * (1.0f / (float)(T * D));
+      mean = (mean < FP16_MAX) ? mean : FP16_MAX;
+      if (lane == 0) sbc = mean;
+    }
+    __syncthreads();
+    if (tid < D) {
+      const uint32_t s16 = f32_to_f16_rne(sbc);
+      const float s32 = f16_to_f32(s16);
+      uint32_t wd[2 * W];
+#pragma unroll
+      for (int i = 0; i < 2 * W; ++i) wd[i] = 0u;
+      float e = 0.f;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float u = yr[t] + e;
+        const bool bt = u >= 0.f;
+        e = u - (bt ? s32 : -s32);
+        wd[t >> 5] |= (uint32_t)bt << (t & 31);
+      }
+      const int64_t slot = seg * out_tile_stride + out_tile_offset + tile;
+      uint64_t* out = bits + slot * (int64_t)(D * W);
+#pragma unroll
+      for (int w = 0; w < W; ++w) out[tid * W + w] = ((uint64_t)wd[2 * w + 1] << 32) | wd[2 * w];
+      if (tid == 0) scales[slot] = (uint16_t)s16;
+    }
+    __syncthreads();  // ys and sbc are rewritten by the next tile
+  }
+}
+
 template <int DT, int TF>
 static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h, int64_t n_tok,
                                   int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
@@ -277,7 +420,15 @@ static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h
   const int64_t nblk = n_b * n_h * n_tiles;
   if (nblk == 0) return hipSuccess;
   dim3 grid((unsigned)nblk), block(64);
-  if (T == 64 && TF != KVR_DCT)
+  if (DT == KVR_BF16 && TF == KVR_DCT) {
+    const dim3 pgrid((unsigned)(nblk < DCT_ENC_BLOCKS ? nblk : DCT_ENC_BLOCKS));
+    if (T == 64)
+      hipLaunchKernelGGL(encode_dct_mfma_kernel<64>, pgrid, dim3(256), 0, s, (const uint16_t*)x, n_h, n_tiles,
+                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, nblk);
+    else
+      hipLaunchKernelGGL(encode_dct_mfma_kernel<128>, pgrid, dim3(256), 0, s, (const uint16_t*)x, n_h, n_tiles,
+                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, nblk);
+  } else if (T == 64 && TF != KVR_DCT)
     hipLaunchKernelGGL((encode_tiles64_kernel<DT, TF == KVR_DCT ? KVR_NONE : TF>), grid, block, 0, s, x,
                        n_h, n_tiles, n_tok, sb, sh, st, bits, scales, ots, oto, dbg);
   else if (T == 64)
