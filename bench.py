@@ -192,23 +192,34 @@ def kernel_breakdown(wl, steps):
             "attn_ms": t_attn}
 
 
-def encode_benchmark(steps):
-    """32 layers x 8 KV heads x 16384 tokens, bf16 K (RoPE, outliers) and V."""
-    L, Hkv, N, T = 32, 8, 16384, 64
-    K, V = make_kv(L, Hkv, N, 100, "cuda")
-    kb, ks = H.alloc_store(L * Hkv, N // T, T, "cuda")
-    vb, vs = H.alloc_store(L * Hkv, N // T, T, "cuda")
+def encode_benchmark(steps, n_seq=32, Hkv=8, N=16384, T=64, tf=H.HADAMARD):
+    """Encode K and V (bf16, K with RoPE and outlier channels) of n_seq sequences (or layers)
+    x Hkv heads x N tokens into 1-bit tiles; returns (ms per K+V pair, bytes moved)."""
+    K, V = make_kv(n_seq, Hkv, N, 100, "cuda")
+    kb, ks = H.alloc_store(n_seq * Hkv, N // T, T, "cuda")
+    vb, vs = H.alloc_store(n_seq * Hkv, N // T, T, "cuda")
 
     def run():
-        H.encode_tiles(K, T, H.HADAMARD, bits=kb, scales=ks)
-        H.encode_tiles(V, T, H.HADAMARD, bits=vb, scales=vs)
+        H.encode_tiles(K, T, tf, bits=kb, scales=ks)
+        H.encode_tiles(V, T, tf, bits=vb, scales=vs)
 
     ms = time_events(run, steps, 2)
-    nbytes = 2 * L * Hkv * N * D * 2 + 2 * L * Hkv * N * D // 8 + 2 * L * Hkv * (N // T) * 2
+    nbytes = 2 * n_seq * Hkv * N * D * 2 + 2 * n_seq * Hkv * N * D // 8 + 2 * n_seq * Hkv * (N // T) * 2
     del K, V, kb, vb
     torch.cuda.empty_cache()
+    return ms, nbytes
+
+
+def encode_results(steps):
+    """configs[1] (32 layers x 8 KV heads x 16384 tokens, Hadamard, T=64) and one layer of
+    configs[4] (B=4 x 4 KV heads x 131072 tokens, DCT-II, T=128)."""
+    ms, nbytes = encode_benchmark(steps)
+    ms4, nbytes4 = encode_benchmark(steps, n_seq=4, Hkv=4, N=131072, T=128, tf=H.DCT)
     return {"encode_config": "configs[1]: 32 layers x 8 KV heads x 16384 tok, K+V bf16 -> 1-bit T=64",
-            "encode_ms": round(ms, 4), "encode_bytes": nbytes, "encode_gbps": round(nbytes / ms / 1e6, 1)}
+            "encode_ms": round(ms, 4), "encode_bytes": nbytes, "encode_gbps": round(nbytes / ms / 1e6, 1),
+            "cfg4_encode_config": "configs[4], one layer: B=4 x 4 KV heads x 131072 tok, K+V bf16 -> DCT-II 1-bit T=128",
+            "cfg4_encode_ms": round(ms4, 4), "cfg4_encode_bytes": nbytes4,
+            "cfg4_encode_gbps": round(nbytes4 / ms4 / 1e6, 1)}
 
 
 def e2e_benchmark(n_prompt=65536, n_new=128, n_layers=32):
@@ -382,9 +393,10 @@ def main():
     if breakdown:
         log("  breakdown (us): " + ", ".join(f"{k}={v * 1e3:.1f}" for k, v in breakdown.items()))
     recall = wl.planted_recall()
-    enc = {} if args.no_encode else encode_benchmark(10)
+    enc = {} if args.no_encode else encode_results(10)
     if enc:
-        log(f"  encode configs[1]: {enc['encode_ms']:.3f} ms, {enc['encode_gbps']} GB/s")
+        log(f"  encode configs[1]: {enc['encode_ms']:.3f} ms, {enc['encode_gbps']} GB/s; "
+            f"configs[4] layer (DCT, T=128): {enc['cfg4_encode_ms']:.3f} ms, {enc['cfg4_encode_gbps']} GB/s")
     e2e = {}
     if args.e2e:
         log(f"configs[3] end-to-end: {args.e2e_layers} layers, prompt {args.e2e_prompt}, {args.e2e_new} new tokens ...")

@@ -10,6 +10,10 @@
 // stride-halving tree, then each lane runs the sigma-delta recurrence for its
 // two channels and writes their uint64 words (coalesced, 512 B per store).
 //
+// Two specialisations below take the common cases: T = 64 with a Hadamard (or no)
+// rotation transposes in two 64-channel halves (half the LDS, twice the waves per CU),
+// and a DCT of bf16 input rotates on MFMA.
+//
 // Replaces the int4/int2 packing of RetrievalIndex.batch_append / append
 // (modules/kvr_retrieval.py:162-207) with the 1-bit tile codec.
 #include "kvr_common.h"
