@@ -86,7 +86,7 @@ def plant_keys(K, q, n_plant, n_ret, Hkv, seed, device):
 
 class DecodeWorkload:
     def __init__(self, B=16, Hq=32, Hkv=8, N=32768, W=1024, T=64, k=32, transform=H.HADAMARD,
-                 device="cuda", seed=0):
+                 device="cuda", seed=0, counts=True):
         self.B, self.Hq, self.Hkv, self.N, self.W, self.T, self.k = B, Hq, Hkv, N, W, T, k
         self.transform = transform
         n_ret = (N - W) // T * T
@@ -96,7 +96,9 @@ class DecodeWorkload:
         self.q = torch.randn((B, Hq, D), generator=g, device=device).to(torch.bfloat16)
         K, V = make_kv(B, Hkv, N, seed, device)
         self.planted = plant_keys(K, self.q, 16, n_ret, Hkv, seed + 2000, device)
-        self.kbits, self.kscale = H.encode_tiles(K[:, :, :n_ret], T, transform)
+        # the K store's per-tile channel counts are written with its tiles (as TileKVCache does)
+        self.kcount = H.alloc_counts(B * Hkv, self.n_tiles, device) if counts else None
+        self.kbits, self.kscale = H.encode_tiles(K[:, :, :n_ret], T, transform, counts=self.kcount)
         self.vbits, self.vscale = H.encode_tiles(V[:, :, :n_ret], T, transform)
         self.win_k = K[:, :, n_ret:].contiguous()
         self.win_v = V[:, :, n_ret:].contiguous()
@@ -109,33 +111,34 @@ class DecodeWorkload:
     def step(self):
         H.decode_step(self.q, self.win_k, self.win_v, self.W, self.kbits, self.vbits, self.kscale,
                       self.vscale, self.n_tiles, self.T, self.transform, self.k, out=self.out,
-                      idx_out=self.idx, workspace=self.ws)
+                      idx_out=self.idx, workspace=self.ws, kcounts=self.kcount)
 
     def make_layers(self, n_layers):
         """n_layers copies of the layer's stores in separate memory, for a step that rotates
         through them: their total exceeds the 256 MB last-level (MALL) cache, so each step
         reads its layer from HBM, as in a multi-layer decode."""
-        self.layers = [(self.win_k, self.win_v, self.kbits, self.vbits, self.kscale, self.vscale)]
+        self.layers = [(self.win_k, self.win_v, self.kbits, self.vbits, self.kscale, self.vscale, self.kcount)]
         for _ in range(n_layers - 1):
-            self.layers.append(tuple(t.clone() for t in self.layers[0]))
+            self.layers.append(tuple(None if t is None else t.clone() for t in self.layers[0]))
         self._li = 0
         torch.cuda.synchronize()
 
     def step_rotating(self):
-        wk, wv, kb, vb, ks, vs = self.layers[self._li]
+        wk, wv, kb, vb, ks, vs, kc = self.layers[self._li]
         self._li = (self._li + 1) % len(self.layers)
         H.decode_step(self.q, wk, wv, self.W, kb, vb, ks, vs, self.n_tiles, self.T, self.transform, self.k,
-                      out=self.out, idx_out=self.idx, workspace=self.ws)
+                      out=self.out, idx_out=self.idx, workspace=self.ws, kcounts=kc)
 
     def window_flops(self):
         """MFMA work of the window part: QK and PV, 2 flop per multiply-add."""
         return 4 * self.B * self.Hq * self.W * D
 
     def algorithmic_bytes(self):
-        """Per step: all K bits scanned + K,V bits and fp16 scales of the selected tiles +
-        bf16 window K,V + bf16 q in and out."""
+        """Per step: the scoring scan (every K tile's 128 channel counts, or all K bits when the
+        step scores from the bits) + K,V bits and fp16 scales of the selected tiles + bf16
+        window K,V + bf16 q in and out."""
         BH, T, W = self.B * self.Hkv, self.T, self.W
-        scan = self.n_tiles * T * D // 8
+        scan = self.n_tiles * D if self.kcount is not None else self.n_tiles * T * D // 8
         sel = 2 * self.k * T * D // 8 + 2 * 2 * self.k
         win = 2 * W * D * 2
         qo = 2 * self.B * self.Hq * D * 2
@@ -364,6 +367,12 @@ def main():
     total, comp = wl.algorithmic_bytes()
     step_gbps = total / ms / 1e6
     log(f"  decode step {ms * 1e3:.1f} us  ({step_gbps:.0f} GB/s algorithmic)")
+    # the same step scoring from the K bits instead of the per-tile channel counts
+    kc, wl.kcount = wl.kcount, None
+    bits_ms = time_events(wl.step, args.steps, args.warmup)
+    bits_total, _ = wl.algorithmic_bytes()
+    wl.kcount = kc
+    log(f"  decode step scoring from the K bits: {bits_ms * 1e3:.1f} us ({bits_total / bits_ms / 1e6:.0f} GB/s algorithmic)")
 
     # the same step with each step's layer read from HBM (4 layers of stores > the MALL)
     cold_ms = None
@@ -434,6 +443,9 @@ def main():
                   "tokens_per_s_32_layers": round(wl.B / (ms / 1e3) / 32, 1),
                   "window_mfma_tflops": round(wl.window_flops() / ms / 1e9, 2),
                   "window_mfma_util_vs_bf16_dense": round(wl.window_flops() / ms / 1e9 / BF16_DENSE_TFLOPS, 5),
+                  "scan_bits_us_per_step": round(bits_ms * 1e3, 2),
+                  "scan_bits_algorithmic_bytes": bits_total,
+                  "scan_bits_gbps": round(bits_total / bits_ms / 1e6, 1),
                   **cfg4, **e2e,
                   "rotating_4_layers_us_per_step": round(cold_ms * 1e3, 2) if cold_ms else None,
                   "rotating_4_layers_gbps": round(total / cold_ms / 1e6, 1) if cold_ms else None, **enc,

@@ -56,14 +56,18 @@ const char* kvr_last_error(void);
  * (strides in elements, channel stride 1).  Segment b*n_h+h writes its tiles to
  * tile slots [out_tile_offset, out_tile_offset + n_tok/T) of a store whose
  * segment pitch is out_tile_stride tiles.  dbg_rotated (nullable) receives the
- * fp32 rotated input, [n_b*n_h][n_tok][128].
+ * fp32 rotated input, [n_b*n_h][n_tok][128].  counts (nullable; same tile slots,
+ * [segment][tile][128] uint8) receives each channel's number of set bits over the
+ * tile's T tokens -- the tile's column sums are 2*count - T, all a tile score reads
+ * (the per-tile chunk summary kvr_decode_step scores from when it is given).
  * Replaces: RetrievalIndex.batch_append / append / _pack_int4 / _pack_int2
  *           (modules/kvr_retrieval.py:187-207, 162-185, 69-91).
  */
 int kvr_encode_tiles(const void* x, int x_dtype, int64_t n_b, int64_t n_h, int64_t n_tok,
                      int64_t stride_b, int64_t stride_h, int64_t stride_t, int d, int T,
                      int transform, uint64_t* bits, uint16_t* scales, int64_t out_tile_stride,
-                     int64_t out_tile_offset, float* dbg_rotated, kvr_stream_t stream);
+                     int64_t out_tile_offset, float* dbg_rotated, uint8_t* counts,
+                     kvr_stream_t stream);
 
 /*
  * Query preparation for B sequences: qbar_rot[b*Hkv+h] = R * mean over the g =
@@ -134,6 +138,9 @@ size_t kvr_decode_step_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, in
  * first n_tiles tiles (with optional per-segment exclusion), top-k, and the
  * fused window + retrieved-tile attention.  idx_out (nullable, [BH][k] int32)
  * receives the selected tiles.  k == 0 or n_tiles == 0 attends the window only.
+ * kcounts (nullable): the K store's per-tile channel counts written by
+ * kvr_encode_tiles (same tile slots); when given, tiles are scored from them (128
+ * bytes per tile instead of the tile's bits; the same scores bit for bit).
  * Replaces: RetrievalIndex.retrieve_topk + the hook's merge
  *           (modules/kvr_retrieval.py:317-412, modules/kvr_hook.py:253-282)
  *           and KVRGenerator.step's attention (modules/kvr_generator.py:100-119).
@@ -142,10 +149,10 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                     const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
                     int64_t win_stride_b, int64_t win_stride_h, int64_t win_stride_t,
                     const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
-                    const uint16_t* vscale, int64_t n_tiles, int64_t tile_stride, int T,
-                    int transform, const int32_t* excl_lo, const int32_t* excl_hi, int k,
-                    void* out, int out_dtype, int32_t* idx_out, void* workspace,
-                    size_t ws_bytes, kvr_stream_t stream);
+                    const uint16_t* vscale, const uint8_t* kcounts, int64_t n_tiles,
+                    int64_t tile_stride, int T, int transform, const int32_t* excl_lo,
+                    const int32_t* excl_hi, int k, void* out, int out_dtype, int32_t* idx_out,
+                    void* workspace, size_t ws_bytes, kvr_stream_t stream);
 
 /*
  * Materialise the tokens of the selected tiles in the original (unrotated)

@@ -13,7 +13,8 @@
 namespace kvr {
 hipError_t launch_encode(int dt, int tf, int T, const void* x, int64_t n_b, int64_t n_h,
                          int64_t n_tok, int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
-                         uint16_t* scales, int64_t ots, int64_t oto, float* dbg, hipStream_t s);
+                         uint16_t* scales, int64_t ots, int64_t oto, float* dbg, uint8_t* counts,
+                         hipStream_t s);
 hipError_t launch_query_prep(int qt, int tf, const void* q, int64_t B, int Hq, int Hkv,
                              float* qbar_rot, float* q_rot, hipStream_t s);
 hipError_t launch_score(int T, int method, const float* qbar_rot, const uint64_t* kbits, int64_t BH,
@@ -24,8 +25,8 @@ hipError_t launch_topk(const float* scores, int64_t BH, int64_t n, int64_t strid
 hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
                          const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
                          const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
-                         const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
-                         const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
+                         const uint16_t* vs, const uint8_t* kc, int64_t n_tiles, int64_t tile_stride,
+                         int T, int tf, const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
                          float* scores, uint64_t* cand, int32_t* idx, float* rec, int32_t* ctr,
                          void* out, int ot, hipStream_t s);
 size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T);
@@ -38,7 +39,7 @@ hipError_t launch_gather(const uint64_t* bits, const uint16_t* scales, int64_t B
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 constexpr int kMaxTopK = 1024;
 constexpr size_t kAlign = 256;
 
@@ -141,7 +142,7 @@ const char* kvr_last_error(void) { return g_last_error.c_str(); }
 int kvr_encode_tiles(const void* x, int x_dtype, int64_t n_b, int64_t n_h, int64_t n_tok,
                      int64_t stride_b, int64_t stride_h, int64_t stride_t, int d, int T,
                      int transform, uint64_t* bits, uint16_t* scales, int64_t out_tile_stride,
-                     int64_t out_tile_offset, float* dbg_rotated, kvr_stream_t stream) {
+                     int64_t out_tile_offset, float* dbg_rotated, uint8_t* counts, kvr_stream_t stream) {
   if (int r = check_common(d, T)) return r;
   if (!valid_dtype(x_dtype)) return fail(KVR_ERR_INVALID, "input dtype %d unknown", x_dtype);
   if (!valid_transform(transform)) return fail(KVR_ERR_INVALID, "transform %d unknown", transform);
@@ -160,11 +161,12 @@ int kvr_encode_tiles(const void* x, int x_dtype, int64_t n_b, int64_t n_h, int64
   if (!aligned(x, 16) || stride_b % vec || stride_h % vec || stride_t % vec)
     return fail(KVR_ERR_ALIGN, "x and its strides must be 16-byte aligned");
   if (stride_b < 0 || stride_h < 0 || stride_t <= 0) return fail(KVR_ERR_INVALID, "bad input strides");
-  if (!aligned(bits, 8) || !aligned(scales, 2) || (dbg_rotated && !aligned(dbg_rotated, 16)))
+  if (!aligned(bits, 8) || !aligned(scales, 2) || (dbg_rotated && !aligned(dbg_rotated, 16)) ||
+      (counts && !aligned(counts, 8)))
     return fail(KVR_ERR_ALIGN, "output pointers misaligned");
   return hip_status(kvr::launch_encode(x_dtype, transform, T, x, n_b, n_h, n_tok, stride_b,
                                        stride_h, stride_t, bits, scales, out_tile_stride,
-                                       out_tile_offset, dbg_rotated, (hipStream_t)stream),
+                                       out_tile_offset, dbg_rotated, counts, (hipStream_t)stream),
                     "kvr_encode_tiles");
 }
 
@@ -260,7 +262,7 @@ int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
   char* ws = (char*)workspace;
   return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
                                        win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
-                                       kscale, vscale, 0, tile_stride, T, transform, nullptr, nullptr,
+                                       kscale, vscale, nullptr, 0, tile_stride, T, transform, nullptr, nullptr,
                                        k, false, nullptr, nullptr, const_cast<int32_t*>(idx),
                                        (float*)(ws + L.rec), nullptr, out, out_dtype,
                                        (hipStream_t)stream),
@@ -278,10 +280,10 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                     const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
                     int64_t win_stride_b, int64_t win_stride_h, int64_t win_stride_t,
                     const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
-                    const uint16_t* vscale, int64_t n_tiles, int64_t tile_stride, int T,
-                    int transform, const int32_t* excl_lo, const int32_t* excl_hi, int k,
-                    void* out, int out_dtype, int32_t* idx_out, void* workspace,
-                    size_t ws_bytes, kvr_stream_t stream) {
+                    const uint16_t* vscale, const uint8_t* kcounts, int64_t n_tiles,
+                    int64_t tile_stride, int T, int transform, const int32_t* excl_lo,
+                    const int32_t* excl_hi, int k, void* out, int out_dtype, int32_t* idx_out,
+                    void* workspace, size_t ws_bytes, kvr_stream_t stream) {
   if (n_tiles < 0) return fail(KVR_ERR_INVALID, "n_tiles < 0");
   if (n_tiles == 0) k = 0;
   if (k > n_tiles) return fail(KVR_ERR_INVALID, "k=%d > n_tiles=%lld", k, (long long)n_tiles);
@@ -292,6 +294,7 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
     return r;
   if ((excl_lo == nullptr) != (excl_hi == nullptr))
     return fail(KVR_ERR_INVALID, "excl_lo and excl_hi must both be given or both NULL");
+  if (kcounts && !aligned(kcounts, 8)) return fail(KVR_ERR_ALIGN, "kcounts must be 8-byte aligned");
   if (B == 0) return KVR_OK;
   const int64_t nt = (k > 0) ? n_tiles : 0;
   const StepLayout L = step_layout(B, Hq, Hkv, win_len, nt, k, T);
@@ -303,8 +306,8 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
   int32_t* idx = idx_out ? idx_out : (int32_t*)(ws + L.idx);
   return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
                                        win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
-                                       kscale, vscale, n_tiles, tile_stride, T, transform, excl_lo,
-                                       excl_hi, k, true, (float*)(ws + L.scores),
+                                       kscale, vscale, kcounts, n_tiles, tile_stride, T, transform,
+                                       excl_lo, excl_hi, k, true, (float*)(ws + L.scores),
                                        (uint64_t*)(ws + L.cand), idx,
                                        (float*)(ws + L.rec), (int32_t*)(ws + L.ctr), out,
                                        out_dtype, (hipStream_t)stream),

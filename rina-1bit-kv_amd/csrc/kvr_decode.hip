@@ -96,6 +96,7 @@ struct DecodeArgs {
   const uint64_t* vbits;
   const uint16_t* kscale;
   const uint16_t* vscale;
+  const uint8_t* kcount;  // per-tile channel counts of the K store (nullable: score from the bits)
   int64_t n_tiles, tile_stride;
   const int32_t* excl_lo;
   const int32_t* excl_hi;
@@ -351,13 +352,35 @@ __device__ __forceinline__ void score_load(const uint64_t* kbits, int64_t seg, i
   }
 }
 
+// A score item's channel counts from the K store's per-tile count summary: lane li of
+// 16-lane group grp reads the 8 bytes of channels 8 li .. 8 li + 7 of its tiles.
+template <int T>
+struct ScoreCounts {
+  uint64_t c[score_tpg(T)];
+};
+
+template <int T>
+__device__ __forceinline__ void counts_load(const uint8_t* kcount, int64_t seg, int64_t tile_stride,
+                                            int64_t t0, int64_t t1, ScoreCounts<T>& sc) {
+  const int grp = threadIdx.x >> 4;
+  const int li = threadIdx.x & 15;
+  const uint8_t* segc = kcount + seg * tile_stride * (int64_t)D;
+#pragma unroll
+  for (int i = 0; i < score_tpg(T); ++i) {
+    int64_t tile = t0 + grp + 16 * i;
+    tile = tile < t1 ? tile : t0;
+    sc.c[i] = *(const uint64_t*)(segc + tile * D + 8 * li);
+  }
+}
+
 // Per-lane sequential fp32 sum of fl(q*c) over its 8 channels, then the 16-lane tree.
-template <int T, int METHOD>
-__device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<T>& sw, int64_t seg,
-                                              int64_t n_tiles, int64_t t0, int64_t t1, int32_t lo,
-                                              int32_t hi, float* scores, uint64_t* lc = nullptr) {
-  constexpr int W = T / 64;
-  constexpr int TPG = ScoreWords<T>::TPG;
+// pcf(i, k): the number of set bits of channel 8 li + k of the lane's tile i (from the
+// words or from the count summary: the same integers, so the same scores).
+template <int T, typename PC>
+__device__ __forceinline__ void score_compute_pc(const float* qs, PC pcf, int64_t seg,
+                                                 int64_t n_tiles, int64_t t0, int64_t t1, int32_t lo,
+                                                 int32_t hi, float* scores, uint64_t* lc) {
+  constexpr int TPG = score_tpg(T);
   const int grp = threadIdx.x >> 4;
   const int li = threadIdx.x & 15;
   float q[8];
@@ -375,9 +398,7 @@ __device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<
     int cc = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      int pc = 0;
-#pragma unroll
-      for (int w = 0; w < W; ++w) pc += count_bits<METHOD>(sw.w[i][k * W + w]);
+      const int pc = pcf(i, k);
       const int c = 2 * pc - T;
       cc += c * c;
       const float prod = q[k] * (float)c;
@@ -404,6 +425,27 @@ __device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<
   if (lc && li == 0)
 #pragma unroll
     for (int i = TPG; i < score_cand_slots(T) / 16; ++i) lc[grp + 16 * i] = 0;  // padding slots
+}
+
+template <int T, int METHOD>
+__device__ __forceinline__ void score_compute(const float* qs, const ScoreWords<T>& sw, int64_t seg,
+                                              int64_t n_tiles, int64_t t0, int64_t t1, int32_t lo,
+                                              int32_t hi, float* scores, uint64_t* lc = nullptr) {
+  constexpr int W = T / 64;
+  score_compute_pc<T>(qs, [&](int i, int k) {
+    int pc = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) pc += count_bits<METHOD>(sw.w[i][k * W + w]);
+    return pc;
+  }, seg, n_tiles, t0, t1, lo, hi, scores, lc);
+}
+
+template <int T>
+__device__ __forceinline__ void score_compute_counts(const float* qs, const ScoreCounts<T>& sc, int64_t seg,
+                                                     int64_t n_tiles, int64_t t0, int64_t t1, int32_t lo,
+                                                     int32_t hi, float* scores, uint64_t* lc) {
+  score_compute_pc<T>(qs, [&](int i, int k) { return (int)((sc.c[i] >> (8 * k)) & 0xffu); },
+                      seg, n_tiles, t0, t1, lo, hi, scores, lc);
 }
 
 // ------------------------------------------------------------------ top-k (one wave)
@@ -1820,11 +1862,19 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int 
   qbar_load<QT>(a, seg, lane, qv0, qv1);
   DctRegs dt{};
   if (a.transform == KVR_DCT) dt = dct_table_load(lane);  // before the words: no wait on them
-  ScoreWords<T> sw;
-  score_load<T>(a.kbits, seg, a.tile_stride, t0, t1, sw);
-  qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane, dt);
-  wave_lds_sync();
-  score_compute<T, 0>(sm.qs[wv], sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
+  if (a.kcount) {  // the count summary: 8 bytes per lane and tile instead of 8 words
+    ScoreCounts<T> sc;
+    counts_load<T>(a.kcount, seg, a.tile_stride, t0, t1, sc);
+    qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane, dt);
+    wave_lds_sync();
+    score_compute_counts<T>(sm.qs[wv], sc, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
+  } else {
+    ScoreWords<T> sw;
+    score_load<T>(a.kbits, seg, a.tile_stride, t0, t1, sw);
+    qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane, dt);
+    wave_lds_sync();
+    score_compute<T, 0>(sm.qs[wv], sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
+  }
   if (a.cand) {
     __syncthreads();
     if (helper) {
@@ -2210,7 +2260,8 @@ static int retrieve_method() {
 hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
                          const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
                          const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
-                         const uint16_t* vs, int64_t n_tiles, int64_t tile_stride, int T, int tf,
+                         const uint16_t* vs, const uint8_t* kc, int64_t n_tiles, int64_t tile_stride,
+                         int T, int tf,
                          const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
                          float* scores, uint64_t* cand, int32_t* idx, float* rec, int32_t* ctr,
                          void* out, int ot, hipStream_t s) {
@@ -2232,6 +2283,7 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   a.vbits = vb;
   a.kscale = ks;
   a.vscale = vs;
+  a.kcount = kc;
   a.n_tiles = n_tiles;
   a.tile_stride = tile_stride;
   a.excl_lo = excl_lo;

@@ -24,7 +24,8 @@ template <int DT, int TF, int T>
 __global__ __launch_bounds__(64) void encode_tiles_kernel(
     const void* __restrict__ x, int64_t n_h, int64_t n_tiles, int64_t n_tok, int64_t stride_b,
     int64_t stride_h, int64_t stride_t, uint64_t* __restrict__ bits, uint16_t* __restrict__ scales,
-    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg) {
+    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg,
+    uint8_t* __restrict__ counts) {
   constexpr int LDW = T + 1;  // padded row: conflict-free column writes and row reads
   constexpr int W = T / 64;
   __shared__ float ys[D * LDW];
@@ -147,6 +148,16 @@ __global__ __launch_bounds__(64) void encode_tiles_kernel(
     out[(lane + 64) * W + w] = ((uint64_t)w1[2 * w + 1] << 32) | w1[2 * w];
   }
   if (lane == 0) scales[slot] = (uint16_t)s16;
+  if (counts) {  // set bits of each channel over the tile's T tokens (at most 128)
+    int p0 = 0, p1 = 0;
+#pragma unroll
+    for (int i = 0; i < 2 * W; ++i) {
+      p0 += __builtin_popcount(w0[i]);
+      p1 += __builtin_popcount(w1[i]);
+    }
+    counts[slot * D + lane] = (uint8_t)p0;
+    counts[slot * D + lane + 64] = (uint8_t)p1;
+  }
 }
 
 // T = 64 with a Hadamard or no rotation: the same codec with half the LDS.  Phase A
@@ -161,7 +172,8 @@ template <int DT, int TF>
 __global__ __launch_bounds__(64) void encode_tiles64_kernel(
     const void* __restrict__ x, int64_t n_h, int64_t n_tiles, int64_t n_tok, int64_t stride_b,
     int64_t stride_h, int64_t stride_t, uint64_t* __restrict__ bits, uint16_t* __restrict__ scales,
-    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg) {
+    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg,
+    uint8_t* __restrict__ counts) {
   static_assert(TF != KVR_DCT, "the DCT rotation uses the full-tile kernel");
   constexpr int T = 64;
   constexpr int H = D / 2;     // channels per transpose half
@@ -270,6 +282,10 @@ __global__ __launch_bounds__(64) void encode_tiles64_kernel(
   out[lane] = ((uint64_t)w0[1] << 32) | w0[0];
   out[lane + 64] = ((uint64_t)w1[1] << 32) | w1[0];
   if (lane == 0) scales[slot] = (uint16_t)s16;
+  if (counts) {  // set bits of each channel over the tile's 64 tokens
+    counts[slot * D + lane] = (uint8_t)(__builtin_popcount(w0[0]) + __builtin_popcount(w0[1]));
+    counts[slot * D + lane + 64] = (uint8_t)(__builtin_popcount(w1[0]) + __builtin_popcount(w1[1]));
+  }
 }
 
 // DCT-II rotation of bf16 input on MFMA, then the same scale and sigma-delta.  Per tile,
@@ -294,7 +310,8 @@ template <int T>
 __global__ __launch_bounds__(256, 2) void encode_dct_mfma_kernel(
     const uint16_t* __restrict__ x, int64_t n_h, int64_t n_tiles, int64_t n_tok, int64_t stride_b,
     int64_t stride_h, int64_t stride_t, uint64_t* __restrict__ bits, uint16_t* __restrict__ scales,
-    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg, int64_t n_blk) {
+    int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg,
+    uint8_t* __restrict__ counts, int64_t n_blk) {
   constexpr int LDW = T + 1;  // padded row
   constexpr int W = T / 64;
   constexpr int NBC = 4;      // 16-token blocks per load batch
@@ -410,6 +427,12 @@ __global__ __launch_bounds__(256, 2) void encode_dct_mfma_kernel(
 #pragma unroll
       for (int w = 0; w < W; ++w) out[tid * W + w] = ((uint64_t)wd[2 * w + 1] << 32) | wd[2 * w];
       if (tid == 0) scales[slot] = (uint16_t)s16;
+      if (counts) {  // set bits of the channel over the tile's T tokens (at most 128)
+        int pc = 0;
+#pragma unroll
+        for (int i = 0; i < 2 * W; ++i) pc += __builtin_popcount(wd[i]);
+        counts[slot * D + tid] = (uint8_t)pc;
+      }
     }
     __syncthreads();  // ys and sbc are rewritten by the next tile
   }
@@ -419,7 +442,7 @@ template <int DT, int TF>
 static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h, int64_t n_tok,
                                   int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
                                   uint16_t* scales, int64_t ots, int64_t oto, float* dbg,
-                                  hipStream_t s) {
+                                  uint8_t* counts, hipStream_t s) {
   const int64_t n_tiles = n_tok / T;
   const int64_t nblk = n_b * n_h * n_tiles;
   if (nblk == 0) return hipSuccess;
@@ -428,29 +451,30 @@ static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h
     const dim3 pgrid((unsigned)(nblk < DCT_ENC_BLOCKS ? nblk : DCT_ENC_BLOCKS));
     if (T == 64)
       hipLaunchKernelGGL(encode_dct_mfma_kernel<64>, pgrid, dim3(256), 0, s, (const uint16_t*)x, n_h, n_tiles,
-                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, nblk);
+                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts, nblk);
     else
       hipLaunchKernelGGL(encode_dct_mfma_kernel<128>, pgrid, dim3(256), 0, s, (const uint16_t*)x, n_h, n_tiles,
-                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, nblk);
+                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts, nblk);
   } else if (T == 64 && TF != KVR_DCT)
     hipLaunchKernelGGL((encode_tiles64_kernel<DT, TF == KVR_DCT ? KVR_NONE : TF>), grid, block, 0, s, x,
-                       n_h, n_tiles, n_tok, sb, sh, st, bits, scales, ots, oto, dbg);
+                       n_h, n_tiles, n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts);
   else if (T == 64)
     hipLaunchKernelGGL((encode_tiles_kernel<DT, TF, 64>), grid, block, 0, s, x, n_h, n_tiles, n_tok,
-                       sb, sh, st, bits, scales, ots, oto, dbg);
+                       sb, sh, st, bits, scales, ots, oto, dbg, counts);
   else
     hipLaunchKernelGGL((encode_tiles_kernel<DT, TF, 128>), grid, block, 0, s, x, n_h, n_tiles,
-                       n_tok, sb, sh, st, bits, scales, ots, oto, dbg);
+                       n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts);
   return hipGetLastError();
 }
 
 hipError_t launch_encode(int dt, int tf, int T, const void* x, int64_t n_b, int64_t n_h,
                          int64_t n_tok, int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
-                         uint16_t* scales, int64_t ots, int64_t oto, float* dbg, hipStream_t s) {
+                         uint16_t* scales, int64_t ots, int64_t oto, float* dbg, uint8_t* counts,
+                         hipStream_t s) {
 #define KVR_ENC(DTV, TFV)                                                                       \
   if (dt == DTV && tf == TFV)                                                                   \
     return launch_encode_t<DTV, TFV>(T, x, n_b, n_h, n_tok, sb, sh, st, bits, scales, ots, oto, \
-                                     dbg, s);
+                                     dbg, counts, s);
   KVR_ENC(KVR_BF16, KVR_HADAMARD)
   KVR_ENC(KVR_FP16, KVR_HADAMARD)
   KVR_ENC(KVR_FP32, KVR_HADAMARD)

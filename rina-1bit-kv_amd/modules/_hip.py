@@ -19,7 +19,7 @@ _DT = {torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32}
 _TORCH_DT = {BF16: torch.bfloat16, FP16: torch.float16, FP32: torch.float32}
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkvr_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -30,7 +30,7 @@ _Z = ctypes.c_size_t
 SIGNATURES = {
     "kvr_abi_version": (_I, []),
     "kvr_last_error": (ctypes.c_char_p, []),
-    "kvr_encode_tiles": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _P, _L, _L, _P, _P]),
+    "kvr_encode_tiles": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _P, _L, _L, _P, _P, _P]),
     "kvr_query_prep": (_I, [_P, _I, _L, _I, _I, _I, _I, _P, _P, _P]),
     "kvr_score_tiles": (_I, [_P, _P, _L, _L, _L, _I, _I, _P, _P, _I, _P, _P]),
     "kvr_topk_tiles": (_I, [_P, _L, _L, _L, _I, _P, _P]),
@@ -38,7 +38,7 @@ SIGNATURES = {
     "kvr_decode_attn": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _P, _P, _P, _P,
                              _L, _I, _I, _P, _I, _P, _I, _P, _Z, _P]),
     "kvr_decode_step_workspace": (_Z, [_L, _I, _I, _L, _L, _I, _I]),
-    "kvr_decode_step": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _P, _P, _P, _P,
+    "kvr_decode_step": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _P, _P, _P, _P, _P,
                              _L, _L, _I, _I, _P, _P, _I, _P, _I, _P, _P, _Z, _P]),
     "kvr_gather_tiles": (_I, [_P, _P, _L, _L, _I, _I, _P, _I, _P, _L, _L, _P]),
 }
@@ -99,15 +99,24 @@ def alloc_store(n_seg: int, tile_cap: int, T: int, device) -> tuple:
     return bits, scales
 
 
+def alloc_counts(n_seg: int, tile_cap: int, device) -> torch.Tensor:
+    """Per-tile channel counts of a K store, uint8 [n_seg, tile_cap, 128], zero-filled: entry
+    (s, i, j) is the number of set bits of channel j over tile i's T tokens (2*count - T is
+    the tile's column sum, all a tile score reads)."""
+    return torch.zeros((n_seg, tile_cap, 128), dtype=torch.uint8, device=device)
+
+
 # ----------------------------------------------------------------------------- encode
 
 def encode_tiles(x: torch.Tensor, T: int, transform: int, bits=None, scales=None, tile_offset: int = 0,
-                 want_rotated: bool = False):
+                 want_rotated: bool = False, counts=None):
     """Encode x [n_b, n_h, n_tok, 128] (last dim contiguous, any other strides) into 1-bit tiles.
 
     Writes tiles [tile_offset, tile_offset + n_tok/T) of each segment b*n_h+h of the store
     (bits [n_b*n_h, cap, 128, T/64] int64, scales [n_b*n_h, cap] fp16), allocating a
-    store of exactly n_tok/T tiles when none is given.  Returns (bits, scales[, rotated]).
+    store of exactly n_tok/T tiles when none is given.  counts (optional, alloc_counts
+    [n_b*n_h, cap, 128] uint8) receives the same tiles' channel counts.  Returns
+    (bits, scales[, rotated]).
     """
     _require_gpu(x)
     if x.dim() != 4 or x.shape[-1] != 128 or x.stride(-1) != 1:
@@ -119,9 +128,13 @@ def encode_tiles(x: torch.Tensor, T: int, transform: int, bits=None, scales=None
     if bits is None:
         bits, scales = alloc_store(n_b * n_h, tile_offset + n_tiles, T, x.device)
     rot = torch.empty((n_b * n_h, n_tok, 128), dtype=torch.float32, device=x.device) if want_rotated else None
+    if counts is not None and (counts.dtype != torch.uint8 or tuple(counts.shape) != (bits.shape[0], bits.shape[1], 128)
+                               or not counts.is_contiguous()):
+        raise ValueError("counts must be a contiguous uint8 [n_seg, tile_cap, 128] tensor matching the store")
     sb, sh, st, _ = x.stride()
     rc = lib().kvr_encode_tiles(_ptr(x), _DT[x.dtype], n_b, n_h, n_tok, sb, sh, st, 128, T, transform,
-                                _ptr(bits), _ptr(scales), bits.shape[1], tile_offset, _ptr(rot), _stream())
+                                _ptr(bits), _ptr(scales), bits.shape[1], tile_offset, _ptr(rot), _ptr(counts),
+                                _stream())
     check(rc, "kvr_encode_tiles")
     return (bits, scales, rot) if want_rotated else (bits, scales)
 
@@ -212,8 +225,14 @@ def decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T, device):
 
 def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles, T, transform, k,
                 excl_lo=None, excl_hi=None, out_dtype=torch.bfloat16, out=None, idx_out=None,
-                workspace=None):
-    """The whole decode hot path for one layer (query prep, scoring, top-k, attention)."""
+                workspace=None, kcounts=None):
+    """The whole decode hot path for one layer (query prep, scoring, top-k, attention).
+    kcounts (optional): the K store's channel counts (alloc_counts, written by encode_tiles);
+    tiles are then scored from them, with the same scores."""
+    if kcounts is not None and (kcounts.dtype != torch.uint8 or kbits is None
+                                or tuple(kcounts.shape) != (kbits.shape[0], kbits.shape[1], 128)
+                                or not kcounts.is_contiguous()):
+        raise ValueError("kcounts must be a contiguous uint8 [n_seg, tile_cap, 128] tensor matching kbits")
     _require_gpu(q)
     q = q.contiguous()
     B, Hq, _ = q.shape
@@ -225,7 +244,8 @@ def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles,
         out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
     tile_stride = kbits.shape[1] if kbits is not None else 1
     rc = lib().kvr_decode_step(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, sb, sh, st,
-                               _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), n_tiles, tile_stride, T,
+                               _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), _ptr(kcounts),
+                               n_tiles, tile_stride, T,
                                transform, _ptr(excl_lo), _ptr(excl_hi), k, _ptr(out), _DT[out.dtype],
                                _ptr(idx_out), _ptr(workspace), workspace.numel(), _stream())
     check(rc, "kvr_decode_step")

@@ -9,6 +9,9 @@ Layout (head-major so every (sequence, KV head) window is one contiguous run in 
                  store is non-empty (the retrieval region is a multiple of T tokens).
   kbits, vbits : int64 [B * Hkv, tile_cap, 128, T / 64] (uint64 words, bit t = token t)
   kscale,vscale: fp16  [B * Hkv, tile_cap]
+  kcount       : uint8 [B * Hkv, tile_cap, 128], each K tile's channel counts (set bits over
+                 its T tokens), written with the tile; the decode step scores tiles from it
+                 (128 bytes per tile instead of the tile's 128 * T / 8).
 When an append fills the window to W + T tokens, its oldest T tokens are encoded into the
 next tile slot straight from a strided view of the window, and the remaining W tokens move
 down by T (one W-token copy per T decode steps).
@@ -36,6 +39,7 @@ class TileKVCache:
         self.n_tiles = 0
         self.kbits, self.kscale = _hip.alloc_store(batch * n_kv, tile_cap, tile, device)
         self.vbits, self.vscale = _hip.alloc_store(batch * n_kv, tile_cap, tile, device)
+        self.kcount = _hip.alloc_counts(batch * n_kv, tile_cap, device)
         self._ws = None
 
     # ------------------------------------------------------------------ store growth
@@ -49,9 +53,9 @@ class TileKVCache:
             new = torch.zeros((old.shape[0], new_cap) + tuple(old.shape[2:]), dtype=old.dtype, device=old.device)
             new[:, :cap] = old
             setattr(self, name, new)
-        for name in ("kscale", "vscale"):
+        for name in ("kscale", "vscale", "kcount"):
             old = getattr(self, name)
-            new = torch.zeros((old.shape[0], new_cap), dtype=old.dtype, device=old.device)
+            new = torch.zeros((old.shape[0], new_cap) + tuple(old.shape[2:]), dtype=old.dtype, device=old.device)
             new[:, :cap] = old
             setattr(self, name, new)
 
@@ -61,7 +65,8 @@ class TileKVCache:
         if m == 0:
             return
         self._ensure_tiles(self.n_tiles + m)
-        _hip.encode_tiles(k, self.T, self.transform, bits=self.kbits, scales=self.kscale, tile_offset=self.n_tiles)
+        _hip.encode_tiles(k, self.T, self.transform, bits=self.kbits, scales=self.kscale, tile_offset=self.n_tiles,
+                          counts=self.kcount)
         _hip.encode_tiles(v, self.T, self.transform, bits=self.vbits, scales=self.vscale, tile_offset=self.n_tiles)
         self.n_tiles += m
 
@@ -108,4 +113,4 @@ class TileKVCache:
             workspace = self._ws
         return _hip.decode_step(q, self.win_k, self.win_v, self.n, self.kbits, self.vbits, self.kscale,
                                 self.vscale, self.n_tiles, self.T, self.transform, k, out_dtype=out_dtype,
-                                out=out, idx_out=idx_out, workspace=workspace)
+                                out=out, idx_out=idx_out, workspace=workspace, kcounts=self.kcount)

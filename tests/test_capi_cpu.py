@@ -60,16 +60,16 @@ def test_validation_errors_without_gpu(lib, H):
     assert lib.kvr_score_tiles(FAKE, FAKE, 1, 4, 4, 100, 64, None, None, 0, FAKE, None) == -1
     assert "head_dim" in H.last_error()
     # T not in {64, 128}
-    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 64, 0, 0, 128, 128, 32, 0, FAKE, FAKE, 2, 0, None, None) == -1
+    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 64, 0, 0, 128, 128, 32, 0, FAKE, FAKE, 2, 0, None, None, None) == -1
     # n_tok not a multiple of T
-    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 100, 0, 0, 128, 128, 64, 0, FAKE, FAKE, 2, 0, None, None) == -1
+    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 100, 0, 0, 128, 128, 64, 0, FAKE, FAKE, 2, 0, None, None, None) == -1
     assert "multiple" in H.last_error()
     # NONE transform needs fp32 input
-    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 64, 0, 0, 128, 128, 64, 2, FAKE, FAKE, 2, 0, None, None) == -1
+    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 64, 0, 0, 128, 128, 64, 2, FAKE, FAKE, 2, 0, None, None, None) == -1
     # tile slots beyond the store
-    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 128, 0, 0, 128, 128, 64, 0, FAKE, FAKE, 2, 1, None, None) == -1
+    assert lib.kvr_encode_tiles(FAKE, 0, 1, 1, 128, 0, 0, 128, 128, 64, 0, FAKE, FAKE, 2, 1, None, None, None) == -1
     # misaligned input
-    assert lib.kvr_encode_tiles(FAKE_MIS, 0, 1, 1, 64, 0, 0, 128, 128, 64, 0, FAKE, FAKE, 2, 0, None, None) == -2
+    assert lib.kvr_encode_tiles(FAKE_MIS, 0, 1, 1, 64, 0, 0, 128, 128, 64, 0, FAKE, FAKE, 2, 0, None, None, None) == -2
     # top-k: k out of range
     assert lib.kvr_topk_tiles(FAKE, 1, 10, 10, 0, FAKE, None) == -1
     assert lib.kvr_topk_tiles(FAKE, 1, 10, 10, 11, FAKE, None) == -1

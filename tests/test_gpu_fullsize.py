@@ -3,7 +3,8 @@
 configs[2] (B=16, GQA 32/8, 32768-token context, bf16 window 1024, Hadamard tiles of 64,
 top-32) and configs[4] (B=4, GQA 28/4, 131072-token context, window 2048, DCT tiles of 128,
 top-64): the one-launch decode step against the CPU oracle on the same stored inputs --
-every segment's selected tiles, and every head's output within the attention tolerance.
+every segment's selected tiles, and every head's output within the attention tolerance --
+scoring from the K store's per-tile channel counts (the product path) and from the bits.
 Encoders at full size (configs[1]: 32 layers x 8 KV heads x 16384 tokens; one configs[4]
 layer: 4 x 4 x 131072 tokens): sampled segments bit-exact against the oracle codec
 (Hadamard from the input, DCT given the kernel's own rotation, which is held to 1e-6 of
@@ -71,20 +72,23 @@ def topk_agree(ig, iref, sref, k, exact):
     "cfg,B,Hq,Hkv,N,W,T,k,tf",
     [("configs[2]", 16, 32, 8, 32768, 1024, 64, 32, O.HADAMARD),
      ("configs[4]", 4, 28, 4, 131072, 2048, 128, 64, O.DCT)])
-@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float32])
-def test_decode_step_full_size(H, cfg, B, Hq, Hkv, N, W, T, k, tf, odt):
-    say(f"[fullsize/decode_step] {cfg} B={B} Hq={Hq} Hkv={Hkv} N={N} W={W} T={T} k={k} out={odt}")
+@pytest.mark.parametrize("odt,use_counts", [(torch.bfloat16, True), (torch.float32, True), (torch.float32, False)])
+def test_decode_step_full_size(H, cfg, B, Hq, Hkv, N, W, T, k, tf, odt, use_counts):
+    say(f"[fullsize/decode_step] {cfg} B={B} Hq={Hq} Hkv={Hkv} N={N} W={W} T={T} k={k} out={odt} "
+        f"counts={use_counts}")
     n_tiles = (N - W) // T
     K = gen_kv((B, Hkv, n_tiles * T, 128), 10)
     V = gen_kv((B, Hkv, n_tiles * T, 128), 11, outliers=False)
-    kb, ks = H.encode_tiles(K, T, tf)
+    counts = H.alloc_counts(B * Hkv, n_tiles, DEV) if use_counts else None
+    kb, ks = H.encode_tiles(K, T, tf, counts=counts)
     vb, vs = H.encode_tiles(V, T, tf)
     del K, V
     wk = gen_kv((B, Hkv, W, 128), 12)
     wv = gen_kv((B, Hkv, W, 128), 13, outliers=False)
     q = gen_kv((B, Hq, 128), 14, outliers=False)
     idx = torch.empty((B * Hkv, k), dtype=torch.int32, device=DEV)
-    out = H.decode_step(q, wk, wv, W, kb, vb, ks, vs, n_tiles, T, tf, k, out_dtype=odt, idx_out=idx)
+    out = H.decode_step(q, wk, wv, W, kb, vb, ks, vs, n_tiles, T, tf, k, out_dtype=odt, idx_out=idx,
+                        kcounts=counts)
     torch.cuda.synchronize()
     kbn, vbn, ksn, vsn = u64(kb), u64(vb), ks.cpu().numpy(), vs.cpu().numpy()
     qn = q.float().cpu().numpy()

@@ -127,6 +127,27 @@ def test_encode_deterministic(H, rng):
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
+@pytest.mark.parametrize("T,tf,dt", [(64, "had", "bf16"), (64, "had", "fp32"), (128, "had", "bf16"),
+                                     (64, "dct", "bf16"), (128, "dct", "bf16"), (128, "dct", "fp32"),
+                                     (64, "none", "fp32")])
+def test_encode_counts_are_channel_popcounts(H, rng, T, tf, dt):
+    """The per-tile channel counts every encoder kernel writes next to the bits equal the
+    number of set bits of each channel word (summed over a T=128 tile's two words), in the
+    same tile slots; slots outside the encoded range stay untouched."""
+    say(f"[encode/counts] T={T} tf={tf} dtype={dt}")
+    tfv = {"had": H.HADAMARD, "dct": H.DCT, "none": H.NONE}[tf]
+    n_b, n_h, n_tok = 2, 3, 5 * T
+    xt = torch.from_numpy(kv_like(rng, (n_b, n_h, n_tok, 128))).to(DEV, TDT[dt])
+    bits, scales = H.alloc_store(n_b * n_h, 7, T, DEV)
+    counts = H.alloc_counts(n_b * n_h, 7, DEV)
+    H.encode_tiles(xt, T, tfv, bits=bits, scales=scales, tile_offset=1, counts=counts)
+    b = u64(bits)  # [seg, tile, 128, T/64]
+    pc = np.unpackbits(b.view(np.uint8), axis=-1).reshape(b.shape + (64,)).sum(axis=(-1, -2))
+    c = counts.cpu().numpy()
+    assert np.array_equal(c[:, 1:6], pc[:, 1:6].astype(np.uint8))
+    assert not c[:, 0].any() and not c[:, 6].any(), "wrote outside its tile slots"
+
+
 # ----------------------------------------------------------------------------- query prep
 
 @pytest.mark.parametrize("Hq,Hkv", [(32, 8), (28, 4), (8, 8)])
@@ -343,6 +364,34 @@ def test_decode_step_matches_oracle_pipeline(H, rng, tf, T, Hq, Hkv, ret_method)
                 assert all(abs(sref[s][t] - kth) <= 1e-6 * np.abs(sref[s]).max() for t in diff)
     ref = O.decode_attention(qn, wk.float().cpu().numpy(), wv.float().cpu().numpy(), kbn, vbn, ksn, vsn, ig, tf)
     check_out(out, ref, "decode_step")
+
+
+@pytest.mark.parametrize("tf,T,Hq,Hkv", [(O.HADAMARD, 64, 32, 8), (O.DCT, 128, 28, 4)])
+def test_decode_step_counts_equal_bits(H, rng, tf, T, Hq, Hkv):
+    """Scoring from the per-tile channel counts gives the same step bit for bit: the same
+    selected tiles and the same output as scoring from the K bits (with an exclusion)."""
+    say(f"[decode_step/counts] tf={tf} T={T}")
+    B, W, n_tok, k = 3, 192, 50 * T, 7
+    K = torch.from_numpy(kv_like(rng, (B, Hkv, n_tok, 128))).to(DEV, torch.bfloat16)
+    V = torch.from_numpy(rng.standard_normal((B, Hkv, n_tok, 128)).astype(np.float32)).to(DEV, torch.bfloat16)
+    counts = H.alloc_counts(B * Hkv, n_tok // T, DEV)
+    kb, ks = H.encode_tiles(K, T, tf, counts=counts)
+    vb, vs = H.encode_tiles(V, T, tf)
+    q = torch.from_numpy(rng.standard_normal((B, Hq, 128)).astype(np.float32)).to(DEV, torch.bfloat16)
+    wk = torch.from_numpy(kv_like(rng, (B, Hkv, W, 128))).to(DEV, torch.bfloat16)
+    wv = torch.from_numpy(rng.standard_normal((B, Hkv, W, 128)).astype(np.float32)).to(DEV, torch.bfloat16)
+    lo = torch.zeros(B * Hkv, dtype=torch.int32, device=DEV)
+    hi = torch.zeros(B * Hkv, dtype=torch.int32, device=DEV)
+    lo[2], hi[2] = 4, 9
+    res = []
+    for kc in (None, counts):
+        idx = torch.empty((B * Hkv, k), dtype=torch.int32, device=DEV)
+        out = H.decode_step(q, wk, wv, W, kb, vb, ks, vs, n_tok // T, T, tf, k, excl_lo=lo, excl_hi=hi,
+                            out_dtype=torch.float32, idx_out=idx, kcounts=kc)
+        torch.cuda.synchronize()
+        res.append((idx.cpu().numpy(), out.cpu().numpy()))
+    assert np.array_equal(res[0][0], res[1][0])
+    assert np.array_equal(res[0][1].view(np.uint32), res[1][1].view(np.uint32))
 
 
 def test_decode_step_workspace_reuse(H, rng):
