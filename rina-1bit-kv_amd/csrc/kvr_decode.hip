@@ -244,7 +244,10 @@ __device__ __forceinline__ void qbar_load(const DecodeArgs& a, int64_t seg, int 
   const int h = (int)(seg - b * a.Hkv);
   const int64_t q0 = (b * a.Hq + (int64_t)h * a.g) * D + 2 * lane;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) q_pair_raw<QT>(a, q0 + (int64_t)(i < a.g ? i : 0) * D, r0[i], r1[i]);
+  for (int i = 0; i < 16; ++i) {  // heads past g are not read (qbar_finish skips them)
+    r0[i] = r1[i] = 0u;
+    if (i < a.g) q_pair_raw<QT>(a, q0 + (int64_t)i * D, r0[i], r1[i]);
+  }
 }
 
 template <int QT>
@@ -391,9 +394,11 @@ __device__ __forceinline__ void score_compute_pc(const float* qs, PC pcf, int64_
   for (int k = 1; k < 8; ++k) qq = qq + q[k] * q[k];
   qq = tree16(qq);
   const float qn = sqrt_rn(qq) + EPS;
+  static_assert(TPG <= 16, "one lane of the group per tile");
+  float dsel = 0.f;
+  int csel = 0;
 #pragma unroll
   for (int i = 0; i < TPG; ++i) {
-    const int64_t tile = t0 + grp + 16 * i;
     float dot = 0.f;
     int cc = 0;
 #pragma unroll
@@ -404,27 +409,33 @@ __device__ __forceinline__ void score_compute_pc(const float* qs, PC pcf, int64_
       const float prod = q[k] * (float)c;
       dot = (k == 0) ? prod : dot + prod;
     }
-    dot = tree16(dot);
+    dot = tree16(dot);  // butterflies: every lane of the group holds the same totals
     cc += (int)xor_lane_u<8>((uint32_t)cc);
     cc += (int)xor_lane_u<4>((uint32_t)cc);
     cc += (int)xor_lane_u<2>((uint32_t)cc);
     cc += (int)xor_lane_u<1>((uint32_t)cc);
-    if (li == 0) {
-      uint64_t cand = 0;  // pads below every real candidate
-      if (tile < t1) {
-        const float cn = sqrt_rn((float)cc) + EPS;
-        float sc = __fdiv_rn(dot, qn * cn);
-        if (sc != sc) sc = -__builtin_inff();
-        if (tile >= lo && tile < hi) sc = -__builtin_inff();
-        scores[seg * n_tiles + tile] = sc;
-        cand = pack_cand(score_key(sc), (uint32_t)tile);
-      }
-      if (lc) lc[grp + 16 * i] = cand;
+    if (li == i) {  // lane i of the group finishes tile i
+      dsel = dot;
+      csel = cc;
     }
   }
-  if (lc && li == 0)
-#pragma unroll
-    for (int i = TPG; i < score_cand_slots(T) / 16; ++i) lc[grp + 16 * i] = 0;  // padding slots
+  // One correctly rounded square root and division per lane for the group's TPG tiles
+  // (lane li: tile t0 + grp + 16 li), instead of one pass per tile on lane 0.
+  const int64_t tile = t0 + grp + 16 * li;
+  if (li < TPG) {
+    uint64_t cand = 0;  // pads below every real candidate
+    if (tile < t1) {
+      const float cn = sqrt_rn((float)csel) + EPS;
+      float sc = __fdiv_rn(dsel, qn * cn);
+      if (sc != sc) sc = -__builtin_inff();
+      if (tile >= lo && tile < hi) sc = -__builtin_inff();
+      scores[seg * n_tiles + tile] = sc;
+      cand = pack_cand(score_key(sc), (uint32_t)tile);
+    }
+    if (lc) lc[grp + 16 * li] = cand;
+  } else if (lc && li < score_cand_slots(T) / 16) {
+    lc[grp + 16 * li] = 0;  // padding slots
+  }
 }
 
 template <int T, int METHOD>
