@@ -73,6 +73,9 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #ifndef KVR_RET_PARTS
 #define KVR_RET_PARTS 2  // fp16 parts of the retrieved MFMA operands q' and sv*P
 #endif
+#ifndef KVR_RET_PRIO
+#define KVR_RET_PRIO 2  // wave issue priority of retrieved items: 0 none, 1 whole role, 2 tile loop
+#endif
 #ifndef KVR_RET_TILES
 #define KVR_RET_TILES 8  // selected tiles per retrieved item (a multiple of 4: one per wave per round)
 #endif
@@ -1493,6 +1496,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int k = a.k;
   const int64_t b = seg / a.Hkv;
   const int64_t h = seg - b * a.Hkv;
+  if (KVR_RET_PRIO == 1) __builtin_amdgcn_s_setprio(3);
 
   // Wave w takes the selected tiles j = rs*4 + w, then + 4*RS, ..., as a sequence of
   // 64-token units (tile j0 + (u / W) * jstep, word u % W); the first unit's words are
@@ -1588,6 +1592,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   for (int i = 0; i < 8; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -__builtin_inff(), l_run = 0.f;
 
+  if (KVR_RET_PRIO == 2) __builtin_amdgcn_s_setprio(3);
   for (int u = 0; u < n_units; ++u) {
     MfmaUnit nxt;  // the wave's next unit, fetched while this one is processed
     if (u + 1 < n_units)
@@ -1668,6 +1673,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     cur = nxt;
   }
 
+  if (KVR_RET_PRIO == 2) __builtin_amdgcn_s_setprio(0);
   // ---- combine the 4 waves into one record (o' in the rotated domain); ow overlays
   // all of the role's scratch, dead once every wave has left the tile loop
   __syncthreads();
@@ -1676,6 +1682,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   // oacc[cb][r] of lane (n, kg) is channel 16 cb + 4 kg + r
   combine_record(oacc, m_run, l_run, sm.u.ow, sm.cs, g, R,
                  [](int i, int r, int kgv) { return 16 * i + 4 * kgv + r; });
+  if (KVR_RET_PRIO == 1) __builtin_amdgcn_s_setprio(0);
 }
 
 // ------------------------------------------------------------------ merge
