@@ -65,7 +65,7 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #define KVR_SCORE_TPG 6  // tiles per 16-lane group of a score item at T = 64: 4, 6 or 8
 #endif
 #ifndef KVR_SCORE_TPG128  // the same at T = 128 (two words per channel)
-#define KVR_SCORE_TPG128 2
+#define KVR_SCORE_TPG128 4
 #endif
 #ifndef KVR_CTR_STRIDE
 #define KVR_CTR_STRIDE 32  // int32 words between per-segment counters (32: a 128-byte line each)
