@@ -62,7 +62,7 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #define KVR_STEP_ORDER 1
 #endif
 #ifndef KVR_SCORE_TPG
-#define KVR_SCORE_TPG 6  // tiles per 16-lane group of a score item at T = 64: 4, 6 or 8
+#define KVR_SCORE_TPG 8  // tiles per 16-lane group of a score item at T = 64: 4, 6 or 8
 #endif
 #ifndef KVR_SCORE_TPG128  // the same at T = 128 (two words per channel)
 #define KVR_SCORE_TPG128 4
