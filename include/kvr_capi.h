@@ -13,7 +13,8 @@
  *            t/64 is the sigma-delta bit of token t of that channel.
  *   scales : fp16 bit patterns [n_seg][tile_stride], one per tile, K and V
  *            in separate arrays.
- *   window : bf16 or fp16 [.. strides ..][W][128], the exact recent tokens.
+ *   window : bf16, fp16 or fp32 [.. strides ..][slots][128], the exact recent
+ *            tokens (a plain run of slots, or a ring).
  *
  * Reference interfaces replaced (paths relative to Misaka477/RINA-1bit-KV):
  *   see the comment above each function.
@@ -36,13 +37,14 @@ enum kvr_status {
   KVR_ERR_ALIGN = -2,       /* pointer not aligned as the kernel requires    */
   KVR_ERR_WORKSPACE = -3,   /* workspace missing or too small                */
   KVR_ERR_HIP = -4,         /* a HIP launch failed                           */
-  KVR_ERR_UNSUPPORTED = -5  /* valid request outside what is built (g > 16) */
+  KVR_ERR_UNSUPPORTED = -5  /* valid request outside what is built (g > 16, ...) */
 };
 
 enum kvr_dtype { KVR_BF16 = 0, KVR_FP16 = 1, KVR_FP32 = 2 };
 enum kvr_transform { KVR_HADAMARD = 0, KVR_DCT = 1, KVR_NONE = 2 };
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature change; 3 added the ring
+ * window, the live state, kvr_cache_append and kvr_set_wait_limit). */
 int kvr_abi_version(void);
 
 /* Thread-local description of the last error returned on this thread. */
@@ -106,53 +108,104 @@ int kvr_topk_tiles(const float* scores, int64_t BH, int64_t n_tiles, int64_t sco
 /* Workspace bytes kvr_decode_attn needs for these sizes.  A decode workspace (either
  * entry point) must be zeroed before its first call and is then reused across calls;
  * it begins with a 1,048,832-byte counter region the calls keep from one call to the
- * next (its first int32 is a sticky error word, set if a bounded wait gave up); the
- * rest is scratch.  Calls that run concurrently need their own workspaces. */
+ * next, the rest is scratch.  The int32 at byte offset 0 is the workspace's sticky
+ * STATUS word: nonzero once a bounded wait inside a decode step gave up (that call's
+ * affected outputs are NaN); every call since the workspace was zeroed is then
+ * suspect, and the workspace must be zeroed again before further use.  Calls that
+ * run concurrently need their own workspaces. */
 size_t kvr_decode_attn_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T);
 
 /*
  * Decode attention for one query token per sequence: one softmax over the
- * first win_len window tokens and the k*T tokens of tiles idx[s][0..k), with
- * logits scaled by 1/sqrt(128).  Retrieved keys/values are s*(2b-1) in the
- * rotated domain; their output is rotated back.  q: [B][Hq][128] (bf16 or
- * fp32); window element (b, h, t, j) at win[b*win_stride_b + h*win_stride_h +
- * t*win_stride_t + j]; out: [B][Hq][128] in out_dtype (bf16 or fp32).
+ * win_len window tokens and the k*T tokens of tiles idx[s][0..k), with logits
+ * scaled by 1/sqrt(128).  Retrieved keys/values are s*(2b-1) in the rotated
+ * domain; their output is rotated back.  q: [B][Hq][128] (bf16, fp16 or fp32);
+ * window slot element (b, h, t, j) at win[b*win_stride_b + h*win_stride_h +
+ * t*win_stride_t + j] (bf16, fp16 or fp32); the window's tokens are slots
+ * [0, win_len), or, for a ring (win_cap > 0), slots (win_start + i) mod win_cap,
+ * i < win_len.  out: [B][Hq][128] in out_dtype (bf16 or fp32).
  * 1 <= Hq/Hkv <= 16.  win_len == 0 or k == 0 disables that part.
- * Replaces: run_fused_attn (modules/kvr_triton.py:94-104) and the attention
- *           merge of the hook (modules/kvr_hook.py:274-282).
+ * Replaces: run_fused_attn (modules/kvr_triton.py:94-104), WindowBuffer.attention
+ *           (modules/kvr_window.py:43-69) and the attention merge of the hook
+ *           (modules/kvr_hook.py:274-282).
  */
 int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
                     const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
-                    int64_t win_stride_b, int64_t win_stride_h, int64_t win_stride_t,
-                    const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
-                    const uint16_t* vscale, int64_t tile_stride, int T, int transform,
-                    const int32_t* idx, int k, void* out, int out_dtype, void* workspace,
-                    size_t ws_bytes, kvr_stream_t stream);
+                    int64_t win_start, int64_t win_cap, int64_t win_stride_b, int64_t win_stride_h,
+                    int64_t win_stride_t, const uint64_t* kbits, const uint64_t* vbits,
+                    const uint16_t* kscale, const uint16_t* vscale, int64_t tile_stride, int T,
+                    int transform, const int32_t* idx, int k, void* out, int out_dtype,
+                    void* workspace, size_t ws_bytes, kvr_stream_t stream);
 
-/* Workspace bytes kvr_decode_step needs for these sizes (zeroed before first use, as above). */
+/* Workspace bytes kvr_decode_step needs for these sizes (zeroed before first use, as
+ * above; with a live state pass the capacities). */
 size_t kvr_decode_step_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles,
                                  int k, int T);
 
 /*
  * The whole decode hot path for one layer: query prep, tile scoring over the
  * first n_tiles tiles (with optional per-segment exclusion), top-k, and the
- * fused window + retrieved-tile attention.  idx_out (nullable, [BH][k] int32)
- * receives the selected tiles.  k == 0 or n_tiles == 0 attends the window only.
- * kcounts (nullable): the K store's per-tile channel counts written by
- * kvr_encode_tiles (same tile slots); when given, tiles are scored from them (128
- * bytes per tile instead of the tile's bits; the same scores bit for bit).
+ * fused window + retrieved-tile attention (window as in kvr_decode_attn).
+ * idx_out (nullable, [BH][k] int32) receives the selected tiles.  k == 0 or
+ * n_tiles == 0 attends the window only.  kcounts (nullable): the K store's
+ * per-tile channel counts written by kvr_encode_tiles (same tile slots); when
+ * given, tiles are scored from them (128 bytes per tile instead of the tile's
+ * bits; the same scores bit for bit).
+ * live_state (nullable, int32 [B*Hkv][4] on the device, 16-byte aligned): each
+ * segment's {window length, ring start, tile count, -} as kvr_cache_append keeps
+ * them, read by the kernel, so one captured launch serves every decode step;
+ * win_len and n_tiles are then the capacities the launch is sized for (a live
+ * count above them is clamped), win_start is ignored and win_cap must be the
+ * ring's.  A live state needs the one-launch step (1 <= k <= 64, B*Hkv <= 4096);
+ * with fewer live tiles than k every stored tile is taken (idx -1 past them).
  * Replaces: RetrievalIndex.retrieve_topk + the hook's merge
  *           (modules/kvr_retrieval.py:317-412, modules/kvr_hook.py:253-282)
  *           and KVRGenerator.step's attention (modules/kvr_generator.py:100-119).
  */
 int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
                     const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
-                    int64_t win_stride_b, int64_t win_stride_h, int64_t win_stride_t,
-                    const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
-                    const uint16_t* vscale, const uint8_t* kcounts, int64_t n_tiles,
-                    int64_t tile_stride, int T, int transform, const int32_t* excl_lo,
-                    const int32_t* excl_hi, int k, void* out, int out_dtype, int32_t* idx_out,
+                    int64_t win_start, int64_t win_cap, int64_t win_stride_b, int64_t win_stride_h,
+                    int64_t win_stride_t, const uint64_t* kbits, const uint64_t* vbits,
+                    const uint16_t* kscale, const uint16_t* vscale, const uint8_t* kcounts,
+                    int64_t n_tiles, int64_t tile_stride, int T, int transform,
+                    const int32_t* excl_lo, const int32_t* excl_hi, int k,
+                    const int32_t* live_state, void* out, int out_dtype, int32_t* idx_out,
                     void* workspace, size_t ws_bytes, kvr_stream_t stream);
+
+/*
+ * Append one token per segment to a per-layer cache: a ring window of W + T slots
+ * (window layout as in kvr_decode_attn, any of bf16 / fp16 / fp32) plus the
+ * K / V tile stores (and, nullable, the K channel counts).  k_new, v_new:
+ * [B][Hkv][128] in new_dtype (post-RoPE K), converted to the window dtype (RNE).
+ * state: int32 [B*Hkv][4] on the device, per segment {n, start, n_tiles, error}:
+ * the window holds n tokens from ring slot start on (W <= n < W + T once the
+ * store is non-empty) and the store n_tiles tiles.  When the new token fills the
+ * ring (n + 1 == W + T) its oldest T tokens are encoded into tile slot n_tiles
+ * (same bits as kvr_encode_tiles on them), start advances by T and n drops to W.
+ * error (sticky): 1 = the state was invalid (nothing written), 2 = the store was
+ * full (tile_stride tiles; the evicted tokens were dropped).  W must be a
+ * positive multiple of T.  Everything happens on the device, so the call can be
+ * captured in a graph.
+ * Replaces: KVRHook._update_stores (modules/kvr_hook.py:136-148) with
+ *           WindowBuffer.append (modules/kvr_window.py:19-25) and
+ *           RetrievalIndex.append (modules/kvr_retrieval.py:162-185).
+ */
+int kvr_cache_append(const void* k_new, const void* v_new, int new_dtype, int64_t B, int Hkv, int d,
+                     void* win_k, void* win_v, int win_dtype, int64_t win_stride_b,
+                     int64_t win_stride_h, int64_t win_stride_t, int64_t W, int T, int transform,
+                     uint64_t* kbits, uint64_t* vbits, uint16_t* kscale, uint16_t* vscale,
+                     uint8_t* kcounts, int64_t tile_stride, int32_t* state, kvr_stream_t stream);
+
+/*
+ * Bounded waits of later decode launches (process-wide): polls before a wait
+ * gives up (0 restores the default, 2^20), and a diagnostic switch that makes
+ * every wait of the one-launch step expect a tag no candidate list carries, so
+ * it gives up after `polls` polls -- for tests of the failure path (status word,
+ * NaN outputs) in which every kernel still ends normally.
+ * Replaces: nothing in the reference (its fallbacks are silent,
+ *           modules/kvr_retrieval.py:13-24); a testing and diagnostic hook.
+ */
+int kvr_set_wait_limit(int polls, int force_give_up);
 
 /*
  * Materialise the tokens of the selected tiles in the original (unrotated)

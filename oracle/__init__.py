@@ -13,7 +13,6 @@ kvr_oracle : numpy restatement of every kernel of the path (transform, tile
              attention), emulating the kernels' fp32 operation order where the
              contract is bit-exact and computing in float64 where it is a
              tolerance.
-datagen    : seeded synthetic inputs for the BASELINE configs.
 
 Pinning status of each oracle function is listed in ``kvr_oracle.__doc__``.
 """

@@ -5,55 +5,39 @@
 
 #include <cstdarg>
 #include <cstdint>
+#include <atomic>
 #include <cstdio>
 #include <string>
 
 #include "../../include/kvr_capi.h"
-
-namespace kvr {
-hipError_t launch_encode(int dt, int tf, int T, const void* x, int64_t n_b, int64_t n_h,
-                         int64_t n_tok, int64_t sb, int64_t sh, int64_t st, uint64_t* bits,
-                         uint16_t* scales, int64_t ots, int64_t oto, float* dbg, uint8_t* counts,
-                         hipStream_t s);
-hipError_t launch_query_prep(int qt, int tf, const void* q, int64_t B, int Hq, int Hkv,
-                             float* qbar_rot, float* q_rot, hipStream_t s);
-hipError_t launch_score(int T, int method, const float* qbar_rot, const uint64_t* kbits, int64_t BH,
-                        int64_t n_tiles, int64_t tile_stride, const int32_t* excl_lo,
-                        const int32_t* excl_hi, float* scores, hipStream_t s);
-hipError_t launch_topk(const float* scores, int64_t BH, int64_t n, int64_t stride, int k,
-                       int32_t* idx, hipStream_t s);
-hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
-                         const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
-                         const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
-                         const uint16_t* vs, const uint8_t* kc, int64_t n_tiles, int64_t tile_stride,
-                         int T, int tf, const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
-                         float* scores, uint64_t* cand, int32_t* idx, float* rec, int32_t* ctr,
-                         void* out, int ot, hipStream_t s);
-size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T);
-size_t counter_bytes();
-size_t cand_bytes(int64_t B, int Hkv, int64_t n_tiles, int k, int T);
-hipError_t launch_gather(const uint64_t* bits, const uint16_t* scales, int64_t BH,
-                         int64_t tile_stride, int T, int tf, const int32_t* idx, int k, float* out,
-                         int64_t oss, int64_t ost, hipStream_t s);
-}  // namespace kvr
+#include "kvr_internal.h"
 
 namespace {
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 constexpr int kMaxTopK = 1024;
 constexpr size_t kAlign = 256;
 
 thread_local std::string g_last_error;
 
-int fail(int code, const char* fmt, ...) {
+int vfail(int code, const char* fmt, va_list ap) {
   char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
   std::vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
   g_last_error = buf;
   return code;
 }
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  const int r = vfail(code, fmt, ap);
+  va_end(ap);
+  return r;
+}
+
+// Bounded-wait settings of every later decode launch (kvr_set_wait_limit).
+std::atomic<int> g_spin_max{1 << 20};
+std::atomic<int> g_wait_fail{0};
 
 int hip_status(hipError_t e, const char* what) {
   if (e == hipSuccess) return KVR_OK;
@@ -81,19 +65,27 @@ int check_heads(int64_t B, int Hq, int Hkv) {
   return KVR_OK;
 }
 
-// Window: 16-byte loads of 8 elements along head_dim.
-int check_window(const void* wk, const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh,
-                 int64_t st) {
+// Window: 16-byte loads along head_dim (8 16-bit or 4 fp32 elements); a ring of win_cap
+// slots holds the win_len valid tokens from slot win_start on.
+int check_window(const void* wk, const void* wv, int wdt, int64_t win_len, int64_t win_start, int64_t win_cap,
+                 int64_t sb, int64_t sh, int64_t st) {
   if (win_len < 0) return fail(KVR_ERR_INVALID, "win_len=%lld < 0", (long long)win_len);
-  if (win_len == 0) return KVR_OK;
-  if (wdt != KVR_BF16 && wdt != KVR_FP16)
-    return fail(KVR_ERR_INVALID, "window dtype %d unsupported (bf16 or fp16)", wdt);
+  if (win_cap < 0) return fail(KVR_ERR_INVALID, "win_cap=%lld < 0", (long long)win_cap);
+  if (win_cap > 0 && win_len > win_cap)
+    return fail(KVR_ERR_INVALID, "win_len=%lld exceeds the ring capacity %lld", (long long)win_len,
+                (long long)win_cap);
+  if (win_start < 0 || (win_cap > 0 ? win_start >= win_cap : win_start != 0))
+    return fail(KVR_ERR_INVALID, "win_start=%lld outside the ring (capacity %lld; 0 without a ring)",
+                (long long)win_start, (long long)win_cap);
+  if (win_len == 0 && win_cap == 0) return KVR_OK;
+  if (!valid_dtype(wdt)) return fail(KVR_ERR_INVALID, "window dtype %d unknown", wdt);
   if (!wk || !wv) return fail(KVR_ERR_INVALID, "window pointers are NULL");
   if (!aligned(wk, 16) || !aligned(wv, 16))
     return fail(KVR_ERR_ALIGN, "window pointers must be 16-byte aligned");
-  if (sb < 0 || sh < 0 || st <= 0 || sb % 8 || sh % 8 || st % 8)
-    return fail(KVR_ERR_ALIGN, "window strides (b=%lld h=%lld t=%lld) must be non-negative multiples of 8 elements",
-                (long long)sb, (long long)sh, (long long)st);
+  const int64_t vec = 16 / (int64_t)elem_size(wdt);
+  if (sb < 0 || sh < 0 || st <= 0 || sb % vec || sh % vec || st % vec)
+    return fail(KVR_ERR_ALIGN, "window strides (b=%lld h=%lld t=%lld) must be non-negative multiples of %lld elements",
+                (long long)sb, (long long)sh, (long long)st, (long long)vec);
   return KVR_OK;
 }
 
@@ -219,12 +211,16 @@ size_t kvr_decode_attn_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, in
   return step_layout(B, Hq, Hkv, win_len, 0, k, T).total;
 }
 
-static int attn_checks(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
+}  // extern "C"
+
+namespace {
+
+int attn_checks(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
                        const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
-                       int64_t sb, int64_t sh, int64_t st, const uint64_t* kbits,
-                       const uint64_t* vbits, const uint16_t* kscale, const uint16_t* vscale,
-                       int64_t tile_stride, int T, int transform, int k, void* out,
-                       int out_dtype) {
+                       int64_t win_start, int64_t win_cap, int64_t sb, int64_t sh, int64_t st,
+                       const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
+                       const uint16_t* vscale, int64_t tile_stride, int T, int transform, int k,
+                       void* out, int out_dtype) {
   if (int r = check_common(d, T)) return r;
   if (int r = check_heads(B, Hq, Hkv)) return r;
   if (!valid_dtype(q_dtype)) return fail(KVR_ERR_INVALID, "q dtype %d unknown", q_dtype);
@@ -232,7 +228,7 @@ static int attn_checks(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, i
   if (out_dtype != KVR_BF16 && out_dtype != KVR_FP32)
     return fail(KVR_ERR_INVALID, "out dtype %d unsupported (bf16 or fp32)", out_dtype);
   if (k < 0 || k > kMaxTopK) return fail(KVR_ERR_INVALID, "k=%d out of [0, %d]", k, kMaxTopK);
-  if (int r = check_window(win_k, win_v, win_dtype, win_len, sb, sh, st)) return r;
+  if (int r = check_window(win_k, win_v, win_dtype, win_len, win_start, win_cap, sb, sh, st)) return r;
   if (k > 0)
     if (int r = check_store(kbits, vbits, kscale, vscale, tile_stride)) return r;
   if (B > 0 && (!q || !out)) return fail(KVR_ERR_INVALID, "q and out must be non-NULL");
@@ -241,77 +237,213 @@ static int attn_checks(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, i
   return KVR_OK;
 }
 
-int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
-                    const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
-                    int64_t win_stride_b, int64_t win_stride_h, int64_t win_stride_t,
-                    const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
-                    const uint16_t* vscale, int64_t tile_stride, int T, int transform,
-                    const int32_t* idx, int k, void* out, int out_dtype, void* workspace,
-                    size_t ws_bytes, kvr_stream_t stream) {
-  if (int r = attn_checks(q, q_dtype, B, Hq, Hkv, d, win_k, win_v, win_dtype, win_len,
-                          win_stride_b, win_stride_h, win_stride_t, kbits, vbits, kscale, vscale,
-                          tile_stride, T, transform, k, out, out_dtype))
-    return r;
-  if (k > 0 && !idx) return fail(KVR_ERR_INVALID, "idx must be non-NULL when k > 0");
-  if (B == 0) return KVR_OK;
-  const StepLayout L = step_layout(B, Hq, Hkv, win_len, 0, k, T);
-  if (!workspace || ws_bytes < L.total)
-    return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", L.total,
-                workspace ? ws_bytes : (size_t)0);
-  if (!aligned(workspace, kAlign)) return fail(KVR_ERR_ALIGN, "workspace must be 256-byte aligned");
-  char* ws = (char*)workspace;
-  return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
-                                       win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
-                                       kscale, vscale, nullptr, 0, tile_stride, T, transform, nullptr, nullptr,
-                                       k, false, nullptr, nullptr, const_cast<int32_t*>(idx),
-                                       (float*)(ws + L.rec), nullptr, out, out_dtype,
-                                       (hipStream_t)stream),
-                    "kvr_decode_attn");
+kvr::DecodeLaunch base_launch(const void* q, int q_dtype, int64_t B, int Hq, int Hkv,
+                                     const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
+                                     int64_t win_start, int64_t win_cap, int64_t sb, int64_t sh, int64_t st,
+                                     const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
+                                     const uint16_t* vscale, int64_t tile_stride, int T, int transform, int k,
+                                     void* out, int out_dtype) {
+  kvr::DecodeLaunch L{};
+  L.qt = q_dtype;
+  L.q = q;
+  L.B = B;
+  L.Hq = Hq;
+  L.Hkv = Hkv;
+  const bool win = win_len > 0 || win_cap > 0;
+  L.wk = win ? win_k : nullptr;
+  L.wv = win ? win_v : nullptr;
+  L.wdt = win ? win_dtype : KVR_BF16;
+  L.win_len = win_len;
+  L.win_start = win_start;
+  L.win_cap = win_cap;
+  L.sb = sb;
+  L.sh = sh;
+  L.st = st;
+  L.kb = kbits;
+  L.vb = vbits;
+  L.ks = kscale;
+  L.vs = vscale;
+  L.tile_stride = tile_stride;
+  L.T = T;
+  L.tf = transform;
+  L.k = k;
+  L.out = out;
+  L.ot = out_dtype;
+  L.spin_max = g_spin_max.load(std::memory_order_relaxed);
+  L.wait_fail = g_wait_fail.load(std::memory_order_relaxed);
+  return L;
 }
 
-size_t kvr_decode_step_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles,
-                                 int k, int T) {
+}  // namespace
+
+namespace kvr {
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  const int r = vfail(code, fmt, ap);
+  va_end(ap);
+  return r;
+}
+
+size_t decode_step_workspace_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles, int k, int T) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || n_tiles < 0 || (T != 64 && T != 128)) return 0;
   if (n_tiles == 0) k = 0;
   return step_layout(B, Hq, Hkv, win_len, k > 0 ? n_tiles : 0, k, T).total;
 }
 
-int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
-                    const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
-                    int64_t win_stride_b, int64_t win_stride_h, int64_t win_stride_t,
-                    const uint64_t* kbits, const uint64_t* vbits, const uint16_t* kscale,
-                    const uint16_t* vscale, const uint8_t* kcounts, int64_t n_tiles,
-                    int64_t tile_stride, int T, int transform, const int32_t* excl_lo,
-                    const int32_t* excl_hi, int k, void* out, int out_dtype, int32_t* idx_out,
-                    void* workspace, size_t ws_bytes, kvr_stream_t stream) {
+int decode_step_impl(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
+                     const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
+                     int64_t win_start, int64_t win_cap, int64_t win_stride_b, int64_t win_stride_h,
+                     int64_t win_stride_t, const uint64_t* kbits, const uint64_t* vbits,
+                     const uint16_t* kscale, const uint16_t* vscale, const uint8_t* kcounts,
+                     int64_t n_tiles, int64_t tile_stride, int T, int transform,
+                     const int32_t* excl_lo, const int32_t* excl_hi, int k, const int32_t* live_state,
+                     void* out, int out_dtype, int32_t* idx_out, void* workspace, size_t ws_bytes,
+                     hipStream_t stream) {
   if (n_tiles < 0) return fail(KVR_ERR_INVALID, "n_tiles < 0");
   if (n_tiles == 0) k = 0;
   if (k > n_tiles) return fail(KVR_ERR_INVALID, "k=%d > n_tiles=%lld", k, (long long)n_tiles);
   if (k > 0 && tile_stride < n_tiles) return fail(KVR_ERR_INVALID, "tile_stride < n_tiles");
-  if (int r = attn_checks(q, q_dtype, B, Hq, Hkv, d, win_k, win_v, win_dtype, win_len,
-                          win_stride_b, win_stride_h, win_stride_t, kbits, vbits, kscale, vscale,
+  if (int r = attn_checks(q, q_dtype, B, Hq, Hkv, d, win_k, win_v, win_dtype, win_len, live_state ? 0 : win_start,
+                          win_cap, win_stride_b, win_stride_h, win_stride_t, kbits, vbits, kscale, vscale,
                           tile_stride, T, transform, k, out, out_dtype))
     return r;
   if ((excl_lo == nullptr) != (excl_hi == nullptr))
     return fail(KVR_ERR_INVALID, "excl_lo and excl_hi must both be given or both NULL");
   if (kcounts && !aligned(kcounts, 8)) return fail(KVR_ERR_ALIGN, "kcounts must be 8-byte aligned");
+  if (live_state) {
+    if (!aligned(live_state, 16)) return fail(KVR_ERR_ALIGN, "live_state must be 16-byte aligned");
+    if (win_cap <= 0) return fail(KVR_ERR_INVALID, "a live state needs a ring window (win_cap > 0)");
+    if (!kvr::step_is_fused(B * Hkv, k, true))
+      return fail(KVR_ERR_UNSUPPORTED,
+                  "a live state needs the one-launch step (1 <= k <= 64, B*Hkv <= 4096, MFMA retrieval); k=%d", k);
+  }
   if (B == 0) return KVR_OK;
   const int64_t nt = (k > 0) ? n_tiles : 0;
-  const StepLayout L = step_layout(B, Hq, Hkv, win_len, nt, k, T);
-  if (!workspace || ws_bytes < L.total)
-    return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", L.total,
+  const StepLayout W = step_layout(B, Hq, Hkv, win_len, nt, k, T);
+  if (!workspace || ws_bytes < W.total)
+    return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", W.total,
                 workspace ? ws_bytes : (size_t)0);
   if (!aligned(workspace, kAlign)) return fail(KVR_ERR_ALIGN, "workspace must be 256-byte aligned");
   char* ws = (char*)workspace;
-  int32_t* idx = idx_out ? idx_out : (int32_t*)(ws + L.idx);
-  return hip_status(kvr::launch_decode(q_dtype, q, B, Hq, Hkv, win_k, win_v, win_dtype, win_len,
-                                       win_stride_b, win_stride_h, win_stride_t, kbits, vbits,
-                                       kscale, vscale, kcounts, n_tiles, tile_stride, T, transform,
-                                       excl_lo, excl_hi, k, true, (float*)(ws + L.scores),
-                                       (uint64_t*)(ws + L.cand), idx,
-                                       (float*)(ws + L.rec), (int32_t*)(ws + L.ctr), out,
-                                       out_dtype, (hipStream_t)stream),
-                    "kvr_decode_step");
+  kvr::DecodeLaunch L = base_launch(q, q_dtype, B, Hq, Hkv, win_k, win_v, win_dtype, win_len, win_start, win_cap,
+                                    win_stride_b, win_stride_h, win_stride_t, kbits, vbits, kscale, vscale,
+                                    tile_stride, T, transform, k, out, out_dtype);
+  L.kc = kcounts;
+  L.n_tiles = n_tiles;
+  L.excl_lo = excl_lo;
+  L.excl_hi = excl_hi;
+  L.live = live_state;
+  L.do_select = true;
+  L.scores = (float*)(ws + W.scores);
+  L.cand = (uint64_t*)(ws + W.cand);
+  L.idx = idx_out ? idx_out : (int32_t*)(ws + W.idx);
+  L.rec = (float*)(ws + W.rec);
+  L.ctr = (int32_t*)(ws + W.ctr);
+  return hip_status(kvr::launch_decode(L, stream), "kvr_decode_step");
+}
+
+}  // namespace kvr
+
+extern "C" {
+
+int kvr_decode_attn(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
+                    const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
+                    int64_t win_start, int64_t win_cap, int64_t win_stride_b, int64_t win_stride_h,
+                    int64_t win_stride_t, const uint64_t* kbits, const uint64_t* vbits,
+                    const uint16_t* kscale, const uint16_t* vscale, int64_t tile_stride, int T, int transform,
+                    const int32_t* idx, int k, void* out, int out_dtype, void* workspace,
+                    size_t ws_bytes, kvr_stream_t stream) {
+  if (int r = attn_checks(q, q_dtype, B, Hq, Hkv, d, win_k, win_v, win_dtype, win_len, win_start, win_cap,
+                          win_stride_b, win_stride_h, win_stride_t, kbits, vbits, kscale, vscale,
+                          tile_stride, T, transform, k, out, out_dtype))
+    return r;
+  if (k > 0 && !idx) return fail(KVR_ERR_INVALID, "idx must be non-NULL when k > 0");
+  if (B == 0) return KVR_OK;
+  const StepLayout W = step_layout(B, Hq, Hkv, win_len, 0, k, T);
+  if (!workspace || ws_bytes < W.total)
+    return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", W.total,
+                workspace ? ws_bytes : (size_t)0);
+  if (!aligned(workspace, kAlign)) return fail(KVR_ERR_ALIGN, "workspace must be 256-byte aligned");
+  char* ws = (char*)workspace;
+  kvr::DecodeLaunch L = base_launch(q, q_dtype, B, Hq, Hkv, win_k, win_v, win_dtype, win_len, win_start, win_cap,
+                                    win_stride_b, win_stride_h, win_stride_t, kbits, vbits, kscale, vscale,
+                                    tile_stride, T, transform, k, out, out_dtype);
+  L.idx = const_cast<int32_t*>(idx);
+  L.rec = (float*)(ws + W.rec);
+  return hip_status(kvr::launch_decode(L, (hipStream_t)stream), "kvr_decode_attn");
+}
+
+size_t kvr_decode_step_workspace(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles,
+                                 int k, int T) {
+  return kvr::decode_step_workspace_bytes(B, Hq, Hkv, win_len, n_tiles, k, T);
+}
+
+int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
+                    const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
+                    int64_t win_start, int64_t win_cap, int64_t win_stride_b, int64_t win_stride_h,
+                    int64_t win_stride_t, const uint64_t* kbits, const uint64_t* vbits,
+                    const uint16_t* kscale, const uint16_t* vscale, const uint8_t* kcounts,
+                    int64_t n_tiles, int64_t tile_stride, int T, int transform, const int32_t* excl_lo,
+                    const int32_t* excl_hi, int k, const int32_t* live_state, void* out, int out_dtype,
+                    int32_t* idx_out, void* workspace, size_t ws_bytes, kvr_stream_t stream) {
+  return kvr::decode_step_impl(q, q_dtype, B, Hq, Hkv, d, win_k, win_v, win_dtype, win_len, win_start, win_cap,
+                               win_stride_b, win_stride_h, win_stride_t, kbits, vbits, kscale, vscale, kcounts,
+                               n_tiles, tile_stride, T, transform, excl_lo, excl_hi, k, live_state, out,
+                               out_dtype, idx_out, workspace, ws_bytes, (hipStream_t)stream);
+}
+
+int kvr_cache_append(const void* k_new, const void* v_new, int new_dtype, int64_t B, int Hkv, int d,
+                     void* win_k, void* win_v, int win_dtype, int64_t win_stride_b, int64_t win_stride_h,
+                     int64_t win_stride_t, int64_t W, int T, int transform, uint64_t* kbits, uint64_t* vbits,
+                     uint16_t* kscale, uint16_t* vscale, uint8_t* kcounts, int64_t tile_stride,
+                     int32_t* state, kvr_stream_t stream) {
+  if (int r = check_common(d, T)) return r;
+  if (B < 0 || Hkv <= 0) return fail(KVR_ERR_INVALID, "B=%lld, Hkv=%d", (long long)B, Hkv);
+  if (!valid_dtype(new_dtype)) return fail(KVR_ERR_INVALID, "new-token dtype %d unknown", new_dtype);
+  if (transform != KVR_HADAMARD && transform != KVR_DCT)
+    return fail(KVR_ERR_INVALID, "transform %d unsupported for the cache (Hadamard or DCT)", transform);
+  if (W < T || W % T) return fail(KVR_ERR_INVALID, "window W=%lld must be a positive multiple of T=%d", (long long)W, T);
+  if (W + T > (1ll << 30)) return fail(KVR_ERR_INVALID, "window W=%lld too large", (long long)W);
+  if (int r = check_window(win_k, win_v, win_dtype, W + T, 0, W + T, win_stride_b, win_stride_h, win_stride_t))
+    return r;
+  if (int r = check_store(kbits, vbits, kscale, vscale, tile_stride)) return r;
+  if (tile_stride > (1ll << 30)) return fail(KVR_ERR_INVALID, "tile_stride too large");
+  if (kcounts && !aligned(kcounts, 8)) return fail(KVR_ERR_ALIGN, "kcounts must be 8-byte aligned");
+  if (B == 0) return KVR_OK;
+  if (!k_new || !v_new || !state) return fail(KVR_ERR_INVALID, "k_new, v_new and state must be non-NULL");
+  if (!aligned(state, 16)) return fail(KVR_ERR_ALIGN, "state must be 16-byte aligned");
+  kvr::AppendLaunch L{};
+  L.k_new = k_new;
+  L.v_new = v_new;
+  L.ndt = new_dtype;
+  L.B = B;
+  L.Hkv = Hkv;
+  L.wk = win_k;
+  L.wv = win_v;
+  L.wdt = win_dtype;
+  L.sb = win_stride_b;
+  L.sh = win_stride_h;
+  L.st = win_stride_t;
+  L.W = W;
+  L.T = T;
+  L.tf = transform;
+  L.kb = kbits;
+  L.vb = vbits;
+  L.ks = kscale;
+  L.vs = vscale;
+  L.kc = kcounts;
+  L.tile_stride = tile_stride;
+  L.state = state;
+  return hip_status(kvr::launch_append(L, (hipStream_t)stream), "kvr_cache_append");
+}
+
+int kvr_set_wait_limit(int polls, int force_give_up) {
+  if (polls < 0) return fail(KVR_ERR_INVALID, "polls=%d < 0", polls);
+  g_spin_max.store(polls == 0 ? (1 << 20) : polls, std::memory_order_relaxed);
+  g_wait_fail.store(force_give_up ? 1 : 0, std::memory_order_relaxed);
+  return KVR_OK;
 }
 
 int kvr_gather_tiles(const uint64_t* bits, const uint16_t* scales, int64_t BH, int64_t tile_stride,

@@ -51,6 +51,11 @@ __device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
   else if constexpr (DT == KVR_FP16) return f16_to_f32(((const uint16_t*)p)[i]);
   else return ((const float*)p)[i];
 }
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+  if (dt == KVR_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+  if (dt == KVR_FP16) return f16_to_f32(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
 
 // Correctly rounded fp32 square root: the f64 root of an f32 is correctly
 // rounded to 53 bits, and 53 >= 2*24+2, so rounding it to f32 is correct.

@@ -2,26 +2,34 @@
 // tile scoring, top-k tile selection, fused window + retrieved-tile attention,
 // the log-sum-exp merge, and the materialising tile gather.
 //
-// One decode step (kvr_decode_step) is three launches and no block ever waits for
-// another block inside a launch (an agent-scope fence costs an L2 write-back on
-// gfx950, so cross-block hand-offs inside a kernel are avoided):
-//   score   : one item per (segment, 64 tiles) (segment = sequence x KV head); the
-//             block loads its tile words first, rotates the segment's GQA-mean query
-//             meanwhile, writes fp32 scores and (k <= 64) its tiles sorted by
-//             (score desc, tile asc) as a candidate list.
-//   attend  : per segment, retrieved items (8 selected tiles, two per wave, MFMA on
-//             +-1 operands) followed by window items (up to 512 window tokens; K
-//             into registers, V rows straight into LDS by direct loads, MFMA,
-//             software-pipelined over 32-token chunks).  A retrieved item first
-//             selects the segment's top-k by merging the candidate lists (every
-//             item of the segment computes the same selection).  Both write
-//             partial softmax records.
-//   merge   : log-sum-exp merge of a segment's records, inverse rotation of the
-//             retrieved part, output.
+// The selecting decode step (kvr_decode_step with k <= 64) is ONE launch,
+// step_kernel, whose blocks are its work items in block order (segment = sequence x
+// KV head):
+//   score items     : one per (segment, 128 tiles at T = 64 / 64 at T = 128); the
+//                     block loads the tiles' channel counts (or bits), rotates the
+//                     segment's GQA-mean query meanwhile, and stores its tiles sorted
+//                     by (score desc, tile asc) as a self-validating candidate list.
+//   retrieved items : merge the segment's candidate lists into the top k (reloading
+//                     until every entry carries this call's tag), then attend 8 (T = 64)
+//                     or 4 (T = 128) selected tiles on MFMA with +-1 operands.
+//   window items    : up to 512 exact window tokens each (MFMA; K into registers, V
+//                     rows straight into LDS by direct loads, software-pipelined).
+// Retrieved and window items write partial softmax records and count them into their
+// segment; the item that brings the count to the segment's total merges the segment
+// (log-sum-exp, inverse rotation of the retrieved part) and writes the output.  Blocks
+// therefore do wait for other blocks inside the launch (retrieved items for score
+// items); why every such wait ends is stated above step_kernel.
+// The other entry points (given indices, k > 64, the VALU retrieval variant) run the
+// same roles as a launch chain without cross-block waits: select_score_kernel ->
+// attend_kernel -> merge_kernel.
 //
 // Partial records: per segment s and part p, g*(2+128) floats: m2[g] (running max,
 // log2 units), l[g], o[g][128].  Window parts hold o in the original domain,
 // retrieved parts in the rotated domain (rotated back once per head in the merge).
+// The window may be a ring (win_cap > 0): logical token i of the win_len valid ones is
+// in slot (win_start + i) mod win_cap.  With a live state (decode step only) the
+// window length, ring start and tile count are read per segment from device memory,
+// and the launch's grid covers the capacities the host passed.
 //
 // Reference behaviour followed (Misaka477/RINA-1bit-KV):
 //   GQA mean query          modules/kvr_retrieval.py:270, 296
@@ -33,6 +41,7 @@
 #include <cstdlib>
 
 #include "kvr_common.h"
+#include "kvr_internal.h"
 
 namespace kvr {
 
@@ -92,9 +101,14 @@ constexpr float SCALE_LOG2 = 0.08838834764831845f * LOG2E;  // log2(e) / sqrt(12
 struct DecodeArgs {
   const void* q;
   int q_dtype, Hq, Hkv, g, transform, out_dtype;
-  const uint16_t* wk;
-  const uint16_t* wv;
+  const void* wk;     // window K, V (bf16 / fp16 / fp32 as the role's template says)
+  const void* wv;
   int64_t win_len, sb, sh, st;
+  int64_t win_start, win_cap;  // ring: token i of the window is in slot (win_start + i) mod win_cap (0: no ring)
+  const int32_t* live;  // per segment {win_len, win_start, n_tiles, -} on the device (step only; nullable)
+  int n_chunks_cap, n_wparts_cap;  // grid decomposition (the capacities when live is given)
+  int spin_max;       // polls of a bounded wait before it gives up
+  int wait_fail;      // test hook: waits expect a tag no list carries, so they give up
   const uint64_t* kbits;
   const uint64_t* vbits;
   const uint16_t* kscale;
@@ -185,30 +199,34 @@ __device__ __forceinline__ uint64_t cand_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Candidate lists validate themselves: an entry is stored as two 8-byte halves, each
-// carrying a 32-bit tag of (epoch, segment, list) in its high word, so a reader that
-// finds the expected tag in both halves has this call's entry of that list, whenever
-// it reads -- no completion wait and counter on the writer's side, no poll before the
-// read.  The epoch is per segment (fused step: the segment's epoch word + 1, advanced
-// by the segment's merging item) or CAND_EPOCH_CHAIN when the lists are written by an
-// earlier launch.
+// Candidate lists validate themselves: an entry is stored as two 8-byte halves, the low
+// half carrying the low 32 bits of a 64-bit tag of (epoch, segment, list) in its high
+// word and the high half the tag's high 32 bits, so a reader that finds the expected
+// tag halves in both words has this call's entry of that list, whenever it reads -- no
+// completion wait and counter on the writer's side, no poll before the read.  The tag
+// is a bijective 64-bit mix (the splitmix64 finaliser) of the injective packing
+// epoch | segment << 32 | list << 52 (segment < 2^20, list < 2^12), so entries of any
+// other (epoch, segment, list) -- an earlier call, another workspace layout -- never
+// validate; zeroed memory never does either (the tag is never 0).  The epoch is per
+// segment (fused step: the segment's epoch word + 1, advanced by the segment's merging
+// item) or CAND_EPOCH_CHAIN when the lists are written by an earlier launch.
 constexpr uint32_t CAND_EPOCH_CHAIN = 0xffffffffu;
-__device__ __forceinline__ uint32_t cand_tag(uint32_t epoch, int64_t seg, int list) {
-  uint32_t x = epoch * 0x9e3779b1u ^ (uint32_t)seg * 0x85ebca77u ^ (uint32_t)(list + 1) * 0xc2b2ae3du;
-  x ^= x >> 16;  // murmur3 finaliser
-  x *= 0x85ebca6bu;
-  x ^= x >> 13;
-  x *= 0xc2b2ae35u;
-  x ^= x >> 16;
-  return x ? x : 1u;  // never 0: zeroed memory is never a valid entry
+constexpr uint32_t WAIT_FAIL_EPOCH = 0x5bd1e995u;  // xor-ed into the expected epoch by the wait_fail hook
+__device__ __forceinline__ uint64_t cand_tag(uint32_t epoch, int64_t seg, int list) {
+  uint64_t z = (uint64_t)epoch | ((uint64_t)((uint32_t)seg & 0xfffffu) << 32) |
+               ((uint64_t)((uint32_t)list & 0xfffu) << 52);
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  z ^= z >> 31;
+  return z ? z : 1ull;  // never 0: zeroed memory is never a valid entry
 }
-__device__ __forceinline__ void cand_put(uint64_t* list, int e, uint64_t v, uint32_t tag) {
-  cand_store(list + 2 * e, ((uint64_t)tag << 32) | (v & 0xffffffffull));
-  cand_store(list + 2 * e + 1, ((uint64_t)tag << 32) | (v >> 32));
+__device__ __forceinline__ void cand_put(uint64_t* list, int e, uint64_t v, uint64_t tag) {
+  cand_store(list + 2 * e, (tag << 32) | (v & 0xffffffffull));
+  cand_store(list + 2 * e + 1, (tag & 0xffffffff00000000ull) | (v >> 32));
 }
-__device__ __forceinline__ uint64_t cand_get(const uint64_t* list, int e, uint32_t tag, bool& ok) {
+__device__ __forceinline__ uint64_t cand_get(const uint64_t* list, int e, uint64_t tag, bool& ok) {
   const uint64_t lo = cand_load(list + 2 * e), hi = cand_load(list + 2 * e + 1);
-  ok = ok && (uint32_t)(lo >> 32) == tag && (uint32_t)(hi >> 32) == tag;
+  ok = ok && (uint32_t)(lo >> 32) == (uint32_t)tag && (uint32_t)(hi >> 32) == (uint32_t)(tag >> 32);
   return (hi << 32) | (lo & 0xffffffffull);
 }
 
@@ -432,7 +450,7 @@ __device__ __forceinline__ void score_compute_pc(const float* qs, PC pcf, int64_
       float sc = __fdiv_rn(dsel, qn * cn);
       if (sc != sc) sc = -__builtin_inff();
       if (tile >= lo && tile < hi) sc = -__builtin_inff();
-      scores[seg * n_tiles + tile] = sc;
+      if (scores) scores[seg * n_tiles + tile] = sc;  // not kept by the one-launch step
       cand = pack_cand(score_key(sc), (uint32_t)tile);
     }
     if (lc) lc[grp + 16 * li] = cand;
@@ -602,39 +620,48 @@ __device__ __forceinline__ uint64_t merge_top64(uint64_t a, uint64_t b_rev, int 
 // sel[0..k) from the n_lists descending candidate lists of a segment (k <= 64), 128
 // words per list: a batch of lists is loaded (list 0 in lane order, the others
 // reversed for the merge, clamped), reloaded until every entry carries its tag (the
-// lists' writers may still be running; at most SPIN_MAX reloads, then *err = 1), then
-// merged in order.
-constexpr int SPIN_MAX = 1 << 20;  // polls of a bounded wait before it sets the error flag
+// lists' writers may still be running), then merged in order.  Every wait is bounded:
+// after spin_max polls it gives up, stores 1 into the sticky error word *err and
+// reports the failure to its caller, which poisons its output (NaN) -- a give-up is
+// never a silent wrong answer.
+
+__device__ __forceinline__ void wait_gave_up(int32_t* err, int lane) {
+  if (err && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Waits until one word (the last) of every list c = first + step * i < n_lists carries
 // its tag: one 8-byte load per list and poll, so a waiting wave adds little traffic
-// while the lists' writers run.  At most SPIN_MAX polls, then *err = 1.
-__device__ __forceinline__ void probe_list_set(const uint64_t* lists, int first, int step, int n_lists,
-                                               int lane, uint32_t epoch, int64_t seg, int32_t* err) {
+// while the lists' writers run.  Returns false when it gave up.
+__device__ __forceinline__ bool probe_list_set(const uint64_t* lists, int first, int step, int n_lists,
+                                               int lane, uint32_t epoch, int64_t seg, int32_t* err,
+                                               int spin_max) {
   for (int r0 = first; r0 < n_lists; r0 += 64 * step) {
     const int c = r0 + step * lane;
-    const uint32_t tag = cand_tag(epoch, seg, c);
+    const uint32_t tag_hi = (uint32_t)(cand_tag(epoch, seg, c) >> 32);
     for (int n = 0;; ++n) {
-      const bool ok = c >= n_lists || (uint32_t)(cand_load(lists + (int64_t)c * 128 + 127) >> 32) == tag;
+      const bool ok = c >= n_lists || (uint32_t)(cand_load(lists + (int64_t)c * 128 + 127) >> 32) == tag_hi;
       if (__all(ok)) break;
-      if (n == SPIN_MAX) {
-        if (err && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
+      if (n >= spin_max) {
+        wait_gave_up(err, lane);
+        return false;
       }
       __builtin_amdgcn_s_sleep(2);
     }
   }
+  return true;
 }
 
 // Top 64 (descending, lane order; 0 pads) of the lists c = first + step * i < n_lists of
 // a segment (128 words per list), loaded in batches of 8 (the first list in lane order,
 // the others reversed for the merge) and reloaded until every entry carries its tag
-// (the lists' writers may still be running; at most SPIN_MAX reloads, then *err = 1).
-// The full loads start once probe_list_set has seen every list's last word.
+// (the lists' writers may still be running).  The full loads start once probe_list_set
+// has seen every list's last word.  failed is set when a wait gave up.
 __device__ __forceinline__ uint64_t merge_list_set(const uint64_t* lists, int first, int step, int n_lists,
-                                                   int lane, uint32_t epoch, int64_t seg, int32_t* err) {
+                                                   int lane, uint32_t epoch, int64_t seg, int32_t* err,
+                                                   int spin_max, bool& failed) {
   constexpr int BATCH = 8;
-  if (epoch != CAND_EPOCH_CHAIN) probe_list_set(lists, first, step, n_lists, lane, epoch, seg, err);
+  if (epoch != CAND_EPOCH_CHAIN && !probe_list_set(lists, first, step, n_lists, lane, epoch, seg, err, spin_max))
+    failed = true;
   uint64_t acc = 0;
   for (int c0 = first; c0 < n_lists; c0 += BATCH * step) {
     uint64_t b[BATCH];
@@ -647,8 +674,9 @@ __device__ __forceinline__ uint64_t merge_list_set(const uint64_t* lists, int fi
                         cand_tag(epoch, seg, c), ok);
       }
       if (__all(ok)) break;
-      if (n == SPIN_MAX) {
-        if (err && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (failed || n >= spin_max) {  // after a failed probe: one load, no further waiting
+        wait_gave_up(err, lane);
+        failed = true;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -661,11 +689,14 @@ __device__ __forceinline__ uint64_t merge_list_set(const uint64_t* lists, int fi
 }
 
 // sel[0..k) from the n_lists descending candidate lists of a segment (k <= 64), merged by
-// one wave.
-__device__ __forceinline__ void select_from_cands(const uint64_t* lists, int n_lists, int k, int32_t* sel,
-                                                  int lane, uint32_t epoch, int64_t seg, int32_t* err) {
-  const uint64_t acc = merge_list_set(lists, 0, 1, n_lists, lane, epoch, seg, err);
+// one wave.  Returns true when a wait gave up.
+__device__ __forceinline__ bool select_from_cands(const uint64_t* lists, int n_lists, int k, int32_t* sel,
+                                                  int lane, uint32_t epoch, int64_t seg, int32_t* err,
+                                                  int spin_max) {
+  bool failed = false;
+  const uint64_t acc = merge_list_set(lists, 0, 1, n_lists, lane, epoch, seg, err, spin_max, failed);
   if (lane < k) sel[lane] = (int32_t)cand_tile(acc);
+  return failed;
 }
 
 // Register-resident select for n <= 64*KPL: bitwise (MSB-first) search of tau, the
@@ -820,13 +851,15 @@ __device__ __forceinline__ void topk_wave(const float* row, int64_t n, int k, in
 
 // The k selected tiles of a segment into sel[0..k): from the score items' sorted
 // candidate lists when they were written (k <= 64), else by the wave select over the
-// segment's scores.
-__device__ __forceinline__ void select_tiles(const DecodeArgs& a, int64_t seg, int k, int32_t* sel,
+// segment's scores.  Returns true when a bounded wait gave up.  The lists of a segment
+// sit at the capacity pitch n_chunks_cap (the same as n_chunks without a live state).
+__device__ __forceinline__ bool select_tiles(const DecodeArgs& a, int64_t seg, int k, int32_t* sel,
                                              TopkSmem& tk, int lane, uint32_t epoch = CAND_EPOCH_CHAIN) {
   if (a.cand)
-    select_from_cands(a.cand + seg * a.n_chunks * (int64_t)128, a.n_chunks, k, sel, lane, epoch, seg,
-                      a.ctr ? a.ctr + CTR_ERR_WORD : nullptr);
-  else topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sel, tk, lane);
+    return select_from_cands(a.cand + seg * a.n_chunks_cap * (int64_t)128, a.n_chunks, k, sel, lane, epoch,
+                             seg, a.ctr ? a.ctr + CTR_ERR_WORD : nullptr, a.spin_max);
+  topk_wave(a.scores + seg * a.n_tiles, a.n_tiles, k, sel, tk, lane);
+  return false;
 }
 
 // ------------------------------------------------------------------ MFMA helpers
@@ -874,7 +907,8 @@ constexpr int OW_WAVE = 16 * D;  // floats of one wave's partial o
 
 template <typename DimOf>
 __device__ __forceinline__ void combine_record(const f32x4 (&oacc)[8], float m_run, float l_run, float* ow,
-                                               CombineSmem& cs, int g, float* R, DimOf dim_of) {
+                                               CombineSmem& cs, int g, float* R, DimOf dim_of,
+                                               bool poison = false) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
@@ -912,7 +946,7 @@ __device__ __forceinline__ void combine_record(const f32x4 (&oacc)[8], float m_r
     float acc = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc += ow[v * OW_WAVE + d * 16 + hn] * fast_exp2(cs.cm[v][hn] - muh);
-    rec_store(R + 2 * g + e, acc);
+    rec_store(R + 2 * g + e, poison ? __builtin_nanf("") : acc);  // a poisoned record makes the output NaN
   }
 }
 
@@ -933,6 +967,23 @@ __device__ void write_record_stats(const CombineSmem& cs, float* R, int g, int t
 }
 
 // ------------------------------------------------------------------ window role (MFMA)
+
+// Slot of logical window token tok (0 <= tok < win_len): the ring start is added and
+// wrapped at the ring capacity (win_start < win_cap and win_len <= win_cap).
+__device__ __forceinline__ int64_t win_slot(const DecodeArgs& a, int64_t tok) {
+  const int64_t s = tok + a.win_start;
+  return (a.win_cap > 0 && s >= a.win_cap) ? s - a.win_cap : s;
+}
+
+// Partial record of a segment: window part p at index p, retrieved part r at
+// n_wparts_cap + r, n_wparts_cap + n_rparts records per segment.
+__device__ __forceinline__ float* rec_ptr(const DecodeArgs& a, int64_t seg, int index) {
+  return a.rec + (seg * (a.n_wparts_cap + a.n_rparts) + index) * (int64_t)(a.g * (2 + D));
+}
+
+__device__ __forceinline__ f32x4 mfma16_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 struct WindowSmem {
   union {
@@ -968,8 +1019,8 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
   const int64_t b = seg / a.Hkv;
   const int64_t h = seg - b * a.Hkv;
 
-  const uint16_t* kbase = a.wk + b * a.sb + h * a.sh;
-  const uint16_t* vbase = a.wv + b * a.sb + h * a.sh;
+  const uint16_t* kbase = (const uint16_t*)a.wk + b * a.sb + h * a.sh;
+  const uint16_t* vbase = (const uint16_t*)a.wv + b * a.sb + h * a.sh;
   const int64_t win_len = a.win_len, st = a.st;
   const int64_t t_begin = (int64_t)part * a.win_span;
   const int64_t t_end = (t_begin + a.win_span < win_len) ? t_begin + a.win_span : win_len;
@@ -981,7 +1032,7 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
     for (int tb = 0; tb < 2; ++tb) {
       int64_t tok = c0 + 16 * tb + n;
       tok = tok < win_len ? tok : win_len - 1;  // clamped rows are masked below
-      const uint16_t* kr = kbase + tok * st + 8 * kg;
+      const uint16_t* kr = kbase + win_slot(a, tok) * st + 8 * kg;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) ka[tb][ks] = *(const u32x4*)(kr + 32 * ks);
     }
@@ -989,8 +1040,8 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
     for (int i = 0; i < 8; ++i) {
       int64_t tok = c0 + 4 * i + kg;
       tok = tok < win_len ? tok : win_len - 1;
-      __builtin_amdgcn_global_load_lds((const void*)(vbase + tok * st + 8 * n), (lds_ptr_t)(vs + i * 4 * D),
-                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vbase + win_slot(a, tok) * st + 8 * n),
+                                       (lds_ptr_t)(vs + i * 4 * D), 16, 0, 0);
     }
   };
   int64_t c0 = t_begin + (int64_t)wv_id * WIN_CHUNK;
@@ -1112,10 +1163,131 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 
   l_run += xor16_f(l_run);
   l_run += xor32_f(l_run);
-  float* R = a.rec + (seg * (a.n_wparts + a.n_rparts) + part) * (int64_t)(g * (2 + D));
   // oacc[i][r] of lane (n, kg) is dim 32 kg + 8 r + i
-  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, R,
+  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, rec_ptr(a, seg, part),
                  [](int i, int r, int kgv) { return 32 * kgv + 8 * r + i; });
+}
+
+// fp32 window tokens on fp32 MFMA (v_mfma_f32_16x16x4_f32; fp32 products, fp32
+// accumulation).  Wave w takes 16-token tiles c0 = t_begin + 16 w, + 64, ...  Lane
+// (n = lane & 15, kg = lane >> 4):
+//   S^T[16 tok x 16 heads] = K Q^T over 32 k-steps; k-step s, k-slot kg is channel
+//     32 kg + s, so lane (n, kg) loads channels 32 kg .. 32 kg + 31 of token c0 + n
+//     (A) and holds query head n's same channels (B).
+//   The S^T accumulator of lane (n, kg) holds tokens 4 kg + r of head n; for the PV
+//   product k-step r's k-slot kg is token 4 kg + r, so the probabilities are the B
+//   operand in place, and lane (n, kg) loads V[token 4 kg + r][dims 8 n .. 8 n + 7]
+//   as the A operands of the eight dim blocks j (D row m <-> dim 8 m + j).
+// The record layout matches the 16-bit window role: oacc[j][r] of lane (n, kg) is dim
+// 32 kg + 8 r + j.
+template <int QT>
+__device__ void window_role_f32(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv_id = tid >> 6;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  const int g = a.g;
+  const int64_t b = seg / a.Hkv;
+  const int64_t h = seg - b * a.Hkv;
+  const float* kbase = (const float*)a.wk + b * a.sb + h * a.sh;
+  const float* vbase = (const float*)a.wv + b * a.sb + h * a.sh;
+  const int64_t win_len = a.win_len, st = a.st;
+  const int64_t t_begin = (int64_t)part * a.win_span;
+  const int64_t t_end = (t_begin + a.win_span < win_len) ? t_begin + a.win_span : win_len;
+
+  float qv[32];  // head n (zeros past g), channels 32 kg .. 32 kg + 31
+  {
+    const int64_t qoff = (b * a.Hq + h * g + (n < g ? n : 0)) * D + 32 * kg;
+    uint32_t r0[16], r1[16];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) q_pair_raw<QT>(a, qoff + 2 * p, r0[p], r1[p]);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      pin(r0[p]);
+      if (QT == Q_RUNTIME || QT == KVR_FP32) pin(r1[p]);
+    }
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      q_pair_cvt<QT>(a, r0[p], r1[p], qv[2 * p], qv[2 * p + 1]);
+      if (n >= g) qv[2 * p] = qv[2 * p + 1] = 0.f;
+    }
+  }
+  f32x4 oacc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+
+  for (int64_t c0 = t_begin + 16 * (int64_t)wv_id; c0 < t_end; c0 += 64) {
+    float kv[32];
+    {
+      int64_t tok = c0 + n;
+      tok = tok < win_len ? tok : win_len - 1;  // clamped rows are masked below
+      const float4* kr = (const float4*)(kbase + win_slot(a, tok) * st + 32 * kg);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float4 f = kr[i];
+        kv[4 * i] = f.x;
+        kv[4 * i + 1] = f.y;
+        kv[4 * i + 2] = f.z;
+        kv[4 * i + 3] = f.w;
+      }
+    }
+    float vv[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int64_t tok = c0 + 4 * kg + r;
+      tok = tok < win_len ? tok : win_len - 1;
+      const float4* vr = (const float4*)(vbase + win_slot(a, tok) * st + 8 * n);
+      const float4 f0 = vr[0], f1 = vr[1];
+      vv[r][0] = f0.x; vv[r][1] = f0.y; vv[r][2] = f0.z; vv[r][3] = f0.w;
+      vv[r][4] = f1.x; vv[r][5] = f1.y; vv[r][6] = f1.z; vv[r][7] = f1.w;
+    }
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 32; ++ks) s = mfma16_f32(kv[ks], qv[ks], s);
+    float p[4];
+    float cmax = -__builtin_inff();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t tok = c0 + 4 * kg + r;
+      const float v = (tok < t_end) ? s[r] * SCALE_LOG2 : -__builtin_inff();
+      p[r] = v;
+      cmax = fmaxf(cmax, v);
+    }
+    cmax = fmaxf(cmax, xor16_f(cmax));
+    cmax = fmaxf(cmax, xor32_f(cmax));
+    const float m_new = fmaxf(m_run, cmax);
+    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = fast_exp2(p[r] - m_use);
+      psum += p[r];
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) oacc[j] = oacc[j] * alpha;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) oacc[j] = mfma16_f32(vv[r][j], p[r], oacc[j]);
+  }
+
+  l_run += xor16_f(l_run);
+  l_run += xor32_f(l_run);
+  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, rec_ptr(a, seg, part),
+                 [](int j, int r, int kgv) { return 32 * kgv + 8 * r + j; });
+}
+
+// The window role for the window's dtype.
+template <int WDT, int QS>
+__device__ __forceinline__ void window_item(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
+  if constexpr (WDT == KVR_FP32) window_role_f32<(QS == 1) ? KVR_FP32 : Q_RUNTIME>(a, seg, part, sm);
+  else window_role<WDT, QS, 3>(a, seg, part, sm);
 }
 
 // Query heads h0, h0 + step, ... (up to QH_MAX of them, the slots a wave rotates) of a
@@ -1493,7 +1665,11 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int n = lane & 15;   // head column / token or channel row
   const int kg = lane >> 4;  // k-slot group
   const int g = a.g;
-  const int k = a.k;
+  const int kp = a.k;  // pitch of the idx rows
+  // tiles selected: k, fewer only when a live tile count is below it (then every stored
+  // tile is taken; none at all when the store is empty)
+  const int k = (a.live && a.n_tiles < (int64_t)a.k) ? (int)a.n_tiles : a.k;
+  const bool do_sel = a.do_select && k > 0;
   const int64_t b = seg / a.Hkv;
   const int64_t h = seg - b * a.Hkv;
   if (KVR_RET_PRIO == 1) __builtin_amdgcn_s_setprio(3);
@@ -1507,10 +1683,10 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int n_units = (j0 < k) ? ((k - 1 - j0) / jstep + 1) * W : 0;
   MfmaUnit cur;
   if (!a.do_select) {
-    if (j0 < k) fetch_mfma_unit<T>(a, seg, a.idx[seg * k + j0], 0, lane, cur);
+    if (j0 < k) fetch_mfma_unit<T>(a, seg, a.idx[seg * kp + j0], 0, lane, cur);
     // the tile loop reads every next index from LDS in both modes (one address space:
     // an index read through a pointer that is LDS or global would be a FLAT load)
-    for (int i = tid; i < k; i += NT) sm.u.sel[i] = a.idx[seg * k + i];
+    for (int i = tid; i < k; i += NT) sm.u.sel[i] = a.idx[seg * kp + i];
   }
 
   // Selection (when asked).  From more than 8 candidate lists: every wave first rotates
@@ -1518,17 +1694,19 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   // w, w + 4, ... into a partial top 64; the four partials meet in LDS and every wave
   // merges them (the same result in each) into its own copy of the selection.  From
   // fewer lists (one load batch) or the scores: wave 0 selects while waves 1..3 rotate
-  // the query heads.
-  const bool par = a.do_select && a.cand && a.n_chunks > 8;  // more than one load batch
-  const int qw0 = (a.do_select && !par) ? 1 : 0;
-  const uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
-                                                                __HIP_MEMORY_SCOPE_AGENT) + 1u
-                                 : CAND_EPOCH_CHAIN;  // the lists' tag epoch
-  if (a.do_select && !par && wv_id == 0) {
-    select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane, ep);
+  // the query heads.  A selection whose bounded wait gave up poisons the item's record.
+  const bool par = do_sel && a.cand && a.n_chunks > 8;  // more than one load batch
+  const int qw0 = (do_sel && !par) ? 1 : 0;
+  uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT) + 1u
+                           : CAND_EPOCH_CHAIN;  // the lists' tag epoch
+  if (a.wait_fail && epoch_word) ep ^= WAIT_FAIL_EPOCH;  // test hook: no list carries this tag
+  bool failed = false;
+  if (do_sel && !par && wv_id == 0) {
+    failed = select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane, ep);
     wave_lds_sync();
     if (rs == 0)
-      for (int i = lane; i < k; i += 64) a.idx[seg * k + i] = sm.u.sel[i];
+      for (int i = lane; i < kp; i += 64) a.idx[seg * kp + i] = (i < k) ? sm.u.sel[i] : -1;
   }
   if (wv_id >= qw0) {
     uint32_t r0[QH_MAX], r1[QH_MAX];
@@ -1561,8 +1739,9 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     }
   }
   if (par)
-    sm.u.p.part[wv_id][lane] = merge_list_set(a.cand + seg * a.n_chunks * (int64_t)128, wv_id, 4, a.n_chunks,
-                                              lane, ep, seg, a.ctr ? a.ctr + CTR_ERR_WORD : nullptr);
+    sm.u.p.part[wv_id][lane] = merge_list_set(a.cand + seg * a.n_chunks_cap * (int64_t)128, wv_id, 4, a.n_chunks,
+                                              lane, ep, seg, a.ctr ? a.ctr + CTR_ERR_WORD : nullptr, a.spin_max,
+                                              failed);
   {  // +-1 patterns: entry x, element e = bit e of x
     const int x = tid;
     uint32_t w[4];
@@ -1574,7 +1753,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     }
     sm.u.pm1[x] = u32x4{w[0], w[1], w[2], w[3]};
   }
-  __syncthreads();
+  const bool poison = __syncthreads_or(failed ? 1 : 0) != 0;  // any wave's wait gave up
   const int32_t* sel = sm.u.sel;
   if (par) {
     uint64_t acc = sm.u.p.part[0][lane];
@@ -1582,10 +1761,10 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     for (int w = 1; w < 4; ++w) acc = merge_top64(acc, sm.u.p.part[w][63 - lane], lane);
     sm.u.selw[wv_id][lane] = (int32_t)cand_tile(acc);
     wave_lds_sync();
-    if (wv_id == 0 && rs == 0 && lane < k) a.idx[seg * k + lane] = (int32_t)cand_tile(acc);
+    if (wv_id == 0 && rs == 0 && lane < kp) a.idx[seg * kp + lane] = (lane < k) ? (int32_t)cand_tile(acc) : -1;
     sel = sm.u.selw[wv_id];
   }
-  if (a.do_select && j0 < k) fetch_mfma_unit<T>(a, seg, sel[j0], 0, lane, cur);
+  if (do_sel && j0 < k) fetch_mfma_unit<T>(a, seg, sel[j0], 0, lane, cur);
 
   f32x4 oacc[8];
 #pragma unroll
@@ -1681,7 +1860,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   l_run += xor32_f(l_run);
   // oacc[cb][r] of lane (n, kg) is channel 16 cb + 4 kg + r
   combine_record(oacc, m_run, l_run, sm.u.ow, sm.cs, g, R,
-                 [](int i, int r, int kgv) { return 16 * i + 4 * kgv + r; });
+                 [](int i, int r, int kgv) { return 16 * i + 4 * kgv + r; }, poison);
   if (KVR_RET_PRIO == 1) __builtin_amdgcn_s_setprio(0);
 }
 
@@ -1704,16 +1883,18 @@ __device__ __forceinline__ void merge_parts(const DecodeArgs& a, const float* R0
                                             float& M, float& L, float& w0, float& w1, float& r0, float& r1) {
   const int g = a.g;
   const int n_parts = a.n_wparts + a.n_rparts;
+  const int gap = a.n_wparts_cap - a.n_wparts;  // live window parts < the record slots reserved for them
+  auto pidx = [&](int p) { return p < a.n_wparts ? p : p + gap; };
   for (int p0 = 0; p0 < n_parts; p0 += MAXP) {
     const bool mine = lane < MAXP && p0 + lane < n_parts;  // this lane's part of the batch
-    const float* Rl = R0 + (mine ? p0 + lane : p0) * rs;
+    const float* Rl = R0 + pidx(mine ? p0 + lane : p0) * rs;
     const float pm = rec_load(Rl + i);
     const float pl = rec_load(Rl + g + i);
     float2 po[MAXP];
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
       const int pc = (p0 + p < n_parts) ? p0 + p : n_parts - 1;
-      po[p] = rec_load2(R0 + pc * rs + 2 * g + i * D + 2 * lane);
+      po[p] = rec_load2(R0 + pidx(pc) * rs + 2 * g + i * D + 2 * lane);
     }
     const float Mn = fmaxf(M, wave_max(mine ? pm : -__builtin_inff()));
     const float mu = (Mn == -__builtin_inff()) ? 0.f : Mn;
@@ -1745,7 +1926,7 @@ __device__ __forceinline__ void merge_sums(const DecodeArgs& a, int64_t seg, int
                                            float& w1, float& r0, float& r1) {
   const int n_parts = a.n_wparts + a.n_rparts;
   const int64_t rs = a.g * (2 + D);
-  const float* R0 = a.rec + seg * n_parts * rs;
+  const float* R0 = rec_ptr(a, seg, 0);
   // batches of 8, 16 or 32 parts: no more loads than parts for small segments
   float M = -__builtin_inff();
   L = w0 = w1 = r0 = r1 = 0.f;
@@ -1784,10 +1965,6 @@ struct MergeSmem {
   float wt[D][17];  // window sums
   float inv[16];    // 1 / L per head
 };
-
-__device__ __forceinline__ f32x4 mfma16_f32(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 __device__ void merge_segment_rot(const DecodeArgs& a, int64_t seg, MergeSmem& ms) {
   const int tid = threadIdx.x;
@@ -1905,7 +2082,7 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int 
                             (uint64_t)(uint32_t)__shfl((int)(uint32_t)u, 63 - lane, 64);
         v = merge_top64(v, ur, lane);
       }
-      cand_put(a.cand + (seg * a.n_chunks + chunk) * 128, lane, v, cand_tag(epoch, seg, (int)chunk));
+      cand_put(a.cand + (seg * a.n_chunks_cap + chunk) * 128, lane, v, cand_tag(epoch, seg, (int)chunk));
     }
   }
 }
@@ -1945,14 +2122,13 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs
     seg = blockIdx.x / parts;
     p = (int)(blockIdx.x - seg * parts);
   }
-  const int64_t rs = a.g * (2 + D);
   if (p < a.n_rparts) {
-    float* R = a.rec + (seg * parts + a.n_wparts + p) * rs;
+    float* R = rec_ptr(a, seg, a.n_wparts_cap + p);
     constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
     if constexpr (RM == 0) retrieved_role_mfma<T, QT>(a, seg, p, sm.retm, R);
     else retrieved_role<T, G4, QT>(a, seg, p, sm.ret, R);
   } else {
-    window_role<WDT, QS, 3>(a, seg, p - a.n_rparts, sm.win);
+    window_item<WDT, QS>(a, seg, p - a.n_rparts, sm.win);
   }
 }
 
@@ -2002,43 +2178,64 @@ struct StepSmem {
 };
 
 template <int T, int WDT, int QS>
-__global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a_in) {
   __shared__ StepSmem sm;
   constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
   const int tid = threadIdx.x;
-  const int64_t S = a.n_seg;
-  const int64_t n_score = S * a.n_chunks, n_win = S * a.n_wparts, n_ret = S * a.n_rparts;
-  const int parts = a.n_wparts + a.n_rparts;
+  const int64_t S = a_in.n_seg;
+  // block -> work item, over the capacities (= the live counts without a live state)
+  const int64_t n_score = S * a_in.n_chunks_cap, n_win = S * a_in.n_wparts_cap, n_ret = S * a_in.n_rparts;
+  const int64_t it = blockIdx.x;
+  int64_t seg;
+  int chunk = -1, wp = -1, rp = -1;  // score chunk, window part or retrieved part
+  if (it < n_score) {
+    seg = it / a_in.n_chunks_cap;
+    chunk = (int)(it - seg * a_in.n_chunks_cap);
+  } else {
+    const int64_t j = it - n_score;
+    const int parts_cap = a_in.n_wparts_cap + a_in.n_rparts;
+    if (KVR_STEP_ORDER == 2) {
+      seg = j / parts_cap;
+      const int p = (int)(j - seg * parts_cap);
+      if (p < a_in.n_wparts_cap) wp = p;
+      else rp = p - a_in.n_wparts_cap;
+    } else {
+      const bool win = (KVR_STEP_ORDER == 1) ? (j >= n_ret) : (j < n_win);
+      const int64_t jj = win ? ((KVR_STEP_ORDER == 1) ? j - n_ret : j) : ((KVR_STEP_ORDER == 1) ? j : j - n_win);
+      const int per = win ? a_in.n_wparts_cap : a_in.n_rparts;
+      seg = jj / per;
+      if (win) wp = (int)(jj - seg * per);
+      else rp = (int)(jj - seg * per);
+    }
+  }
+  // The segment's live window length, ring start and tile count (clamped to the
+  // capacities the grid and the buffers were sized for), and what follows from them.
+  DecodeArgs a = a_in;
+  if (a.live) {
+    const int32_t* ls = a.live + seg * 4;
+    const int64_t wl = ls[0], ws = ls[1], nt = ls[2];
+    a.win_len = wl < 0 ? 0 : (wl > a_in.win_len ? a_in.win_len : wl);
+    a.win_start = (ws < 0 || ws >= a.win_cap) ? 0 : ws;
+    a.n_tiles = nt < 0 ? 0 : (nt > a_in.n_tiles ? a_in.n_tiles : nt);
+    a.n_chunks = (int)((a.n_tiles + score_tiles_per_item(T) - 1) / score_tiles_per_item(T));
+    a.n_wparts = (int)((a.win_len + a.win_span - 1) / a.win_span);
+    if (a.n_wparts == 0 && a.n_rparts == 0) a.n_wparts = 1;  // an empty window item still writes the output (zeros)
+  }
   int32_t* epoch = a.ctr + CTR_HDR;                       // [seg * CTR_STRIDE] the segment's epoch
   int32_t* rdone = epoch + STEP_MAX_SEG * CTR_STRIDE;    // [seg * CTR_STRIDE] records done
-  const int64_t it = blockIdx.x;
-  if (it < n_score) {
-    const int64_t seg = it / a.n_chunks;
+  if (chunk >= 0) {
+    if (chunk >= a.n_chunks) return;  // past the live tiles
     const uint32_t ep = (uint32_t)ctr_load(epoch + seg * CTR_STRIDE) + 1u;  // used when the list is stored
-    score_item<T, QT>(a, seg, it - seg * a.n_chunks, (int)(it & 3), sm.u.sc, ep);
+    score_item<T, QT>(a, seg, chunk, (int)(it & 3), sm.u.sc, ep);
     return;
   }
-  const int64_t j = it - n_score;
-  int64_t seg;
-  int wp, rp;  // window part, or retrieved part (wp < 0)
-  if (KVR_STEP_ORDER == 2) {
-    seg = j / parts;
-    const int p = (int)(j - seg * parts);
-    wp = p < a.n_wparts ? p : -1;
-    rp = p - a.n_wparts;
-  } else {
-    const bool win = (KVR_STEP_ORDER == 1) ? (j >= n_ret) : (j < n_win);
-    const int64_t jj = win ? ((KVR_STEP_ORDER == 1) ? j - n_ret : j) : ((KVR_STEP_ORDER == 1) ? j : j - n_win);
-    const int per = win ? a.n_wparts : a.n_rparts;
-    seg = jj / per;
-    wp = win ? (int)(jj - seg * per) : -1;
-    rp = win ? 0 : (int)(jj - seg * per);
-  }
+  if (wp >= a.n_wparts) return;  // past the live window
+  const int parts = a.n_wparts + a.n_rparts;
   if (wp >= 0) {
-    window_role<WDT, QS, 3>(a, seg, wp, sm.u.win);
+    window_item<WDT, QS>(a, seg, wp, sm.u.win);
   } else {
-    float* R = a.rec + (seg * parts + a.n_wparts + rp) * (int64_t)(a.g * (2 + D));
-    retrieved_role_mfma<T, QT>(a, seg, rp, sm.u.retm, R, epoch + seg * CTR_STRIDE);
+    retrieved_role_mfma<T, QT>(a, seg, rp, sm.u.retm, rec_ptr(a, seg, a.n_wparts_cap + rp),
+                               epoch + seg * CTR_STRIDE);
   }
   wait_vm();  // record stored
   __syncthreads();
@@ -2265,78 +2462,95 @@ hipError_t launch_topk(const float* scores, int64_t BH, int64_t n, int64_t strid
 }
 
 // Retrieved-tile arithmetic: MFMA on unpacked +-1 operands (default) or the VALU
-// nibble-table path; KVR_RETRIEVE_METHOD=valu selects the latter (same results
-// within the attention tolerance).
+// nibble-table path, the measured alternative; KVR_RETRIEVE_METHOD=valu selects the
+// latter (same results within the attention tolerance).  A diagnostic switch, read at
+// each launch (a getenv; the tests flip it inside one process).
 static int retrieve_method() {
   const char* e = getenv("KVR_RETRIEVE_METHOD");
   return (e && (e[0] == 'v' || e[0] == 'V')) ? 1 : 0;
 }
 
+// Whether a decode step with these sizes runs as the one-launch step_kernel (the only
+// path that takes a live state).
+bool step_is_fused(int64_t BH, int k, bool have_ctr) {
+  return KVR_FUSED_STEP && have_ctr && k > 0 && k <= KVR_CAND_MAX && k <= 64 && retrieve_method() == 0 &&
+         BH <= STEP_MAX_SEG;
+}
+
 // Full decode.  Selecting with candidate lists: one launch (step_kernel).
 // Otherwise: [score launch when selecting] -> attend launch (retrieved + window items)
-// -> merge launch.
-hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, const void* wk,
-                         const void* wv, int wdt, int64_t win_len, int64_t sb, int64_t sh, int64_t st,
-                         const uint64_t* kb, const uint64_t* vb, const uint16_t* ks,
-                         const uint16_t* vs, const uint8_t* kc, int64_t n_tiles, int64_t tile_stride,
-                         int T, int tf,
-                         const int32_t* excl_lo, const int32_t* excl_hi, int k, bool do_select,
-                         float* scores, uint64_t* cand, int32_t* idx, float* rec, int32_t* ctr,
-                         void* out, int ot, hipStream_t s) {
+// -> merge launch.  With a live state (fused step only) win_len and n_tiles are the
+// capacities; the kernel reads the live values per segment.
+hipError_t launch_decode(const DecodeLaunch& L, hipStream_t s) {
   DecodeArgs a{};
-  a.q = q;
-  a.q_dtype = qt;
-  a.Hq = Hq;
-  a.Hkv = Hkv;
-  a.g = Hq / Hkv;
-  a.transform = tf;
-  a.out_dtype = ot;
-  a.wk = (const uint16_t*)wk;
-  a.wv = (const uint16_t*)wv;
-  a.win_len = win_len;
-  a.sb = sb;
-  a.sh = sh;
-  a.st = st;
-  a.kbits = kb;
-  a.vbits = vb;
-  a.kscale = ks;
-  a.vscale = vs;
-  a.kcount = kc;
-  a.n_tiles = n_tiles;
-  a.tile_stride = tile_stride;
-  a.excl_lo = excl_lo;
-  a.excl_hi = excl_hi;
-  a.k = k;
-  a.scores = scores;
-  a.idx = idx;
-  a.rec = rec;
-  a.n_chunks = (int)((n_tiles + score_tiles_per_item(T) - 1) / score_tiles_per_item(T));
-  a.n_wparts = n_window_parts(B * Hkv, win_len);
-  a.win_span = window_span(B * Hkv, win_len);
-  a.n_rparts = n_retrieved_parts(k, T);
-  a.do_select = (do_select && k > 0) ? 1 : 0;
-  a.cand = (a.do_select && k <= KVR_CAND_MAX && k <= 64) ? cand : nullptr;
+  const int64_t B = L.B;
+  const int T = L.T;
+  a.q = L.q;
+  a.q_dtype = L.qt;
+  a.Hq = L.Hq;
+  a.Hkv = L.Hkv;
+  a.g = L.Hq / L.Hkv;
+  a.transform = L.tf;
+  a.out_dtype = L.ot;
+  a.wk = L.wk;
+  a.wv = L.wv;
+  a.win_len = L.win_len;
+  a.win_start = L.win_start;
+  a.win_cap = L.win_cap;
+  a.live = L.live;
+  a.sb = L.sb;
+  a.sh = L.sh;
+  a.st = L.st;
+  a.kbits = L.kb;
+  a.vbits = L.vb;
+  a.kscale = L.ks;
+  a.vscale = L.vs;
+  a.kcount = L.kc;
+  a.n_tiles = L.n_tiles;
+  a.tile_stride = L.tile_stride;
+  a.excl_lo = L.excl_lo;
+  a.excl_hi = L.excl_hi;
+  a.k = L.k;
+  a.scores = L.scores;
+  a.idx = L.idx;
+  a.rec = L.rec;
+  a.n_chunks = (int)((L.n_tiles + score_tiles_per_item(T) - 1) / score_tiles_per_item(T));
+  a.n_wparts = n_window_parts(B * L.Hkv, L.win_len);
+  a.win_span = window_span(B * L.Hkv, L.win_len);
+  a.n_rparts = n_retrieved_parts(L.k, T);
+  a.n_chunks_cap = a.n_chunks;
+  a.n_wparts_cap = a.n_wparts;
+  a.spin_max = L.spin_max;
+  a.wait_fail = L.wait_fail;
+  a.do_select = (L.do_select && L.k > 0) ? 1 : 0;
+  a.cand = (a.do_select && L.k <= KVR_CAND_MAX && L.k <= 64) ? L.cand : nullptr;
   a.ret_method = retrieve_method();
-  a.out = out;
-  a.ctr = ctr;
-  a.n_seg = B * Hkv;
-  const int64_t BH = B * Hkv;
+  a.out = L.out;
+  a.ctr = L.ctr;
+  a.n_seg = B * L.Hkv;
+  const int64_t BH = B * L.Hkv;
   if (BH == 0) return hipSuccess;
+  const int wdt = L.wdt, qt = L.qt;
   if (a.n_wparts + a.n_rparts == 0) {
-    const int64_t n = B * Hq * D;
+    const int64_t n = B * L.Hq * D;
     hipLaunchKernelGGL(zero_out_kernel, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, a, n);
     return hipGetLastError();
   }
-  if (KVR_FUSED_STEP && ctr && a.cand && a.ret_method == 0 && BH <= STEP_MAX_SEG) {
-    const int64_t tickets = BH * (a.n_chunks + a.n_wparts + a.n_rparts);  // blocks = work items
+  const bool fused = L.do_select && step_is_fused(BH, L.k, L.ctr != nullptr) && a.cand;
+  if (L.live && !fused) return hipErrorInvalidValue;  // the host rejects this before launching
+  if (fused) {
+    a.scores = nullptr;  // the one-launch step keeps no score array
+    const int64_t tickets = BH * (a.n_chunks_cap + a.n_wparts_cap + a.n_rparts);  // blocks = work items
     const bool same = (qt == wdt);
 #define KVR_ST(TV, WV, QSV) \
   hipLaunchKernelGGL((step_kernel<TV, WV, QSV>), dim3((unsigned)tickets), dim3(NT), 0, s, a);
 #define KVR_ST_Q(TV, WV) \
   if (same) KVR_ST(TV, WV, 1) else KVR_ST(TV, WV, 3)
     if (T == 64 && wdt == KVR_FP16) { KVR_ST_Q(64, KVR_FP16) }
+    else if (T == 64 && wdt == KVR_FP32) { KVR_ST_Q(64, KVR_FP32) }
     else if (T == 64) { KVR_ST_Q(64, KVR_BF16) }
     else if (wdt == KVR_FP16) { KVR_ST_Q(128, KVR_FP16) }
+    else if (wdt == KVR_FP32) { KVR_ST_Q(128, KVR_FP32) }
     else { KVR_ST_Q(128, KVR_BF16) }
 #undef KVR_ST_Q
 #undef KVR_ST
@@ -2368,16 +2582,22 @@ hipError_t launch_decode(int qt, const void* q, int64_t B, int Hq, int Hkv, cons
   else KVR_ATT(TV, WV, QSV, 1, 16);
 #define KVR_ATT_Q(TV, WV) \
   if (same) { KVR_ATT_G(TV, WV, 1) } else { KVR_ATT_G(TV, WV, 3) }
+    // an fp32 window takes the MFMA retrieval variant only
+#define KVR_ATT_F32(TV) \
+  if (same) { KVR_ATT(TV, KVR_FP32, 1, 0, 4); } else { KVR_ATT(TV, KVR_FP32, 3, 0, 4); }
     if (T == 64 && wdt == KVR_FP16) { KVR_ATT_Q(64, KVR_FP16) }
+    else if (T == 64 && wdt == KVR_FP32) { KVR_ATT_F32(64) }
     else if (T == 64) { KVR_ATT_Q(64, KVR_BF16) }
     else if (wdt == KVR_FP16) { KVR_ATT_Q(128, KVR_FP16) }
+    else if (wdt == KVR_FP32) { KVR_ATT_F32(128) }
     else { KVR_ATT_Q(128, KVR_BF16) }
+#undef KVR_ATT_F32
 #undef KVR_ATT_Q
 #undef KVR_ATT_G
 #undef KVR_ATT
     if (hipError_t e = hipGetLastError()) return e;
   }
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)(B * Hq)), dim3(64), 0, s, a);
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)(B * L.Hq)), dim3(64), 0, s, a);
   return hipGetLastError();
 }
 

@@ -19,7 +19,7 @@ _DT = {torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32}
 _TORCH_DT = {BF16: torch.bfloat16, FP16: torch.float16, FP32: torch.float32}
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkvr_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -35,12 +35,15 @@ SIGNATURES = {
     "kvr_score_tiles": (_I, [_P, _P, _L, _L, _L, _I, _I, _P, _P, _I, _P, _P]),
     "kvr_topk_tiles": (_I, [_P, _L, _L, _L, _I, _P, _P]),
     "kvr_decode_attn_workspace": (_Z, [_L, _I, _I, _L, _I, _I]),
-    "kvr_decode_attn": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _P, _P, _P, _P,
+    "kvr_decode_attn": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P,
                              _L, _I, _I, _P, _I, _P, _I, _P, _Z, _P]),
     "kvr_decode_step_workspace": (_Z, [_L, _I, _I, _L, _L, _I, _I]),
-    "kvr_decode_step": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _P, _P, _P, _P, _P,
-                             _L, _L, _I, _I, _P, _P, _I, _P, _I, _P, _P, _Z, _P]),
+    "kvr_decode_step": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P, _P,
+                             _L, _L, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _Z, _P]),
     "kvr_gather_tiles": (_I, [_P, _P, _L, _L, _I, _I, _P, _I, _P, _L, _L, _P]),
+    "kvr_cache_append": (_I, [_P, _P, _I, _L, _I, _I, _P, _P, _I, _L, _L, _L, _L, _I, _I, _P, _P, _P, _P, _P,
+                              _L, _P, _P]),
+    "kvr_set_wait_limit": (_I, [_I, _I]),
 }
 
 _lib = None
@@ -180,31 +183,32 @@ def topk_tiles(scores: torch.Tensor, k: int, out=None):
 
 # ----------------------------------------------------------------------------- attention
 
-def _window_args(win_k, win_v, win_len):
-    if win_k is None or win_len == 0:
-        return None, None, BF16, 0, 0, 0, 0
+def _window_args(win_k, win_v, win_len, win_start=0, win_cap=0):
+    if win_k is None or (win_len == 0 and win_cap == 0):
+        return None, None, BF16, 0, 0, 0, 0, 0, 0
     if win_k.stride() != win_v.stride() or win_k.stride(-1) != 1:
         raise ValueError("window K and V need identical strides and a contiguous last dim")
     sb, sh, st, _ = win_k.stride()
-    return win_k, win_v, _DT[win_k.dtype], win_len, sb, sh, st
+    return win_k, win_v, _DT[win_k.dtype], win_len, win_start, win_cap, sb, sh, st
 
 
 def decode_attn(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, idx, T, transform,
-                out_dtype=torch.float32, workspace=None):
-    """Fused window + retrieved-tile attention.  q [B, Hq, 128]; window [B, Hkv, W, 128]."""
+                out_dtype=torch.float32, workspace=None, win_start=0, win_cap=0):
+    """Fused window + retrieved-tile attention.  q [B, Hq, 128]; window [B, Hkv, slots, 128]
+    (tokens in slots [0, win_len), or a ring of win_cap slots from win_start)."""
     _require_gpu(q, win_k, kbits, idx)
     q = q.contiguous()
     B, Hq, _ = q.shape
     Hkv = win_k.shape[1] if win_k is not None else kbits.shape[0] // B
     k = 0 if idx is None else idx.shape[1]
-    wk, wv, wdt, wl, sb, sh, st = _window_args(win_k, win_v, win_len)
+    wk, wv, wdt, wl, w0, wc, sb, sh, st = _window_args(win_k, win_v, win_len, win_start, win_cap)
     need = lib().kvr_decode_attn_workspace(B, Hq, Hkv, wl, k, T)
     if workspace is None or workspace.numel() < need:
         workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=q.device)  # zeroed counter region
     out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
     tile_stride = kbits.shape[1] if kbits is not None else 1
-    rc = lib().kvr_decode_attn(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, sb, sh, st,
-                               _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), tile_stride, T,
+    rc = lib().kvr_decode_attn(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, w0, wc,
+                               sb, sh, st, _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), tile_stride, T,
                                transform, _ptr(idx), k, _ptr(out), _DT[out_dtype], _ptr(workspace),
                                workspace.numel(), _stream())
     check(rc, "kvr_decode_attn")
@@ -225,10 +229,13 @@ def decode_step_workspace(B, Hq, Hkv, win_len, n_tiles, k, T, device):
 
 def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles, T, transform, k,
                 excl_lo=None, excl_hi=None, out_dtype=torch.bfloat16, out=None, idx_out=None,
-                workspace=None, kcounts=None):
+                workspace=None, kcounts=None, win_start=0, win_cap=0, live_state=None):
     """The whole decode hot path for one layer (query prep, scoring, top-k, attention).
     kcounts (optional): the K store's channel counts (alloc_counts, written by encode_tiles);
-    tiles are then scored from them, with the same scores."""
+    tiles are then scored from them, with the same scores.  A ring window: win_cap slots,
+    tokens from win_start on.  live_state (optional, int32 [B*Hkv, 4] device tensor as
+    cache_append keeps it): the kernel reads each segment's window length, ring start and
+    tile count from it, and win_len / n_tiles are the capacities."""
     if kcounts is not None and (kcounts.dtype != torch.uint8 or kbits is None
                                 or tuple(kcounts.shape) != (kbits.shape[0], kbits.shape[1], 128)
                                 or not kcounts.is_contiguous()):
@@ -237,19 +244,74 @@ def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles,
     q = q.contiguous()
     B, Hq, _ = q.shape
     Hkv = win_k.shape[1] if win_k is not None else kbits.shape[0] // B
-    wk, wv, wdt, wl, sb, sh, st = _window_args(win_k, win_v, win_len)
+    if live_state is not None:
+        _check_state(live_state, B * Hkv)
+    wk, wv, wdt, wl, w0, wc, sb, sh, st = _window_args(win_k, win_v, win_len, win_start, win_cap)
     if workspace is None:
         workspace = decode_step_workspace(B, Hq, Hkv, wl, n_tiles, k, T, q.device)
     if out is None:
         out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
     tile_stride = kbits.shape[1] if kbits is not None else 1
-    rc = lib().kvr_decode_step(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, sb, sh, st,
-                               _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), _ptr(kcounts),
-                               n_tiles, tile_stride, T,
-                               transform, _ptr(excl_lo), _ptr(excl_hi), k, _ptr(out), _DT[out.dtype],
-                               _ptr(idx_out), _ptr(workspace), workspace.numel(), _stream())
+    rc = lib().kvr_decode_step(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, w0, wc,
+                               sb, sh, st, _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale), _ptr(kcounts),
+                               n_tiles, tile_stride, T, transform, _ptr(excl_lo), _ptr(excl_hi), k,
+                               _ptr(live_state), _ptr(out), _DT[out.dtype], _ptr(idx_out), _ptr(workspace),
+                               workspace.numel(), _stream())
     check(rc, "kvr_decode_step")
     return out
+
+
+def workspace_status(workspace) -> int:
+    """The workspace's sticky status word (int32 at byte 0; synchronises with the device):
+    nonzero once a bounded wait of a decode step gave up."""
+    return int(workspace[:4].view(torch.int32).item())
+
+
+def check_workspace(workspace, what="decode step"):
+    """Raise RuntimeError if a decode step on this workspace gave up a bounded wait; the
+    workspace is zeroed again first, so it is usable afterwards."""
+    st = workspace_status(workspace)
+    if st != 0:
+        workspace.zero_()
+        raise RuntimeError(f"{what}: a bounded wait gave up (workspace status {st}); the outputs of the calls "
+                           "since the workspace was last zeroed are unreliable (affected ones are NaN)")
+
+
+def set_wait_limit(polls: int = 0, force_give_up: bool = False) -> None:
+    """Bounded-wait polls of later decode launches (0 = default) and the diagnostic switch
+    that makes the one-launch step's waits give up (tests of the failure path)."""
+    check(lib().kvr_set_wait_limit(int(polls), int(bool(force_give_up))), "kvr_set_wait_limit")
+
+
+# ----------------------------------------------------------------------------- ring cache append
+
+STATE_WORDS = 4  # per segment: n (window tokens), start (ring slot), n_tiles, error
+
+
+def _check_state(state, n_seg):
+    if (state.dtype != torch.int32 or tuple(state.shape) != (n_seg, STATE_WORDS) or not state.is_contiguous()
+            or not state.is_cuda):
+        raise ValueError(f"state must be a contiguous int32 [{n_seg}, {STATE_WORDS}] device tensor")
+
+
+def cache_append(k_new, v_new, win_k, win_v, W, T, transform, kbits, vbits, kscale, vscale, kcounts, state):
+    """One token per segment (k_new, v_new [B, Hkv, 128]) into a ring window [B, Hkv, W + T, 128]
+    and, when the ring fills, its oldest T tokens into the next tile slot; state is the
+    int32 [B*Hkv, 4] device tensor {n, start, n_tiles, error} the kernel keeps."""
+    _require_gpu(k_new, v_new, win_k, kbits, state)
+    k_new = k_new.contiguous()
+    v_new = v_new.to(k_new.dtype).contiguous()
+    B, Hkv, _ = k_new.shape
+    _check_state(state, B * Hkv)
+    if win_k.shape[2] != W + T or win_k.stride() != win_v.stride() or win_k.stride(-1) != 1:
+        raise ValueError("the ring window must be [B, Hkv, W + T, 128] with K and V strides equal")
+    if kcounts is not None and tuple(kcounts.shape) != (kbits.shape[0], kbits.shape[1], 128):
+        raise ValueError("kcounts must match the store")
+    sb, sh, st, _ = win_k.stride()
+    rc = lib().kvr_cache_append(_ptr(k_new), _ptr(v_new), _DT[k_new.dtype], B, Hkv, 128, _ptr(win_k), _ptr(win_v),
+                                _DT[win_k.dtype], sb, sh, st, W, T, transform, _ptr(kbits), _ptr(vbits),
+                                _ptr(kscale), _ptr(vscale), _ptr(kcounts), kbits.shape[1], _ptr(state), _stream())
+    check(rc, "kvr_cache_append")
 
 
 def gather_tiles(bits, scales, idx, T, transform, out=None):

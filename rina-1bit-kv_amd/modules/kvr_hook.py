@@ -18,8 +18,17 @@ model(..., logits_to_keep=1).  Batches of B >= 1 equal-length sequences are supp
 Prefill encodes each layer's K/V into tiles inside the capture hook, so no fp32 copy of all
 layers is kept (kvr_hook.py:93-133 kept them all).
 
-Extra kwargs: tile (64 or 128 tokens), transform ('hadamard' or 'dct').  The reference's
-warmup_mode / calibration / MLP adapters are not part of this path.
+Extra kwargs: tile (64 or 128 tokens), transform ('hadamard' or 'dct'), reserve_tokens
+(decode tokens the tile stores are sized for at prefill; default 4096 -- beyond it a store
+grows, which an already captured graph does not follow).  The reference's warmup_mode /
+calibration / MLP adapters are not part of this path.
+
+Per-layer objects: `windows[li]` and `retrievals[li]` are WindowBuffer- / RetrievalIndex-
+compatible views of the layer's TileKVCache (kvr_views.py).  Attention is computed in
+fp32 and rounded once to the model dtype (bf16 models: the kernel writes bf16 directly).
+Failures are loud: every 64th decode step per layer polls the layer's workspace status
+and cache error field without blocking, and `check()` does so synchronously; a bounded
+wait that gave up or an invalid cache state raises RuntimeError.
 """
 from __future__ import annotations
 
@@ -27,6 +36,7 @@ import torch
 
 from . import _hip
 from .kvr_cache import TileKVCache
+from .kvr_views import CacheRetrievalView, CacheWindowView
 
 
 def _rotate_half(x):
@@ -58,6 +68,7 @@ class KVRHook:
         self.chunk_size = kwargs.get('chunk_size', 0)
         self.tile = kwargs.get('tile', 64)
         self.transform = _hip.TRANSFORMS[kwargs.get('transform', 'hadamard')]
+        self.reserve_tokens = int(kwargs.get('reserve_tokens', 4096))  # decode tokens the stores are sized for
         for unsupported in ('warmup_mode',):
             if kwargs.get(unsupported):
                 raise NotImplementedError(f"{unsupported} is not part of the 1-bit KV path")
@@ -68,23 +79,31 @@ class KVRHook:
         self._retrieval_built = False
         self.caches = [None] * self.n_layers
 
-    # The reference exposes per-layer window / index objects; here both are the layer cache.
+    # The reference exposes per-layer WindowBuffer / RetrievalIndex objects (kvr_hook.py:43-47);
+    # here both are views of the layer's TileKVCache (sequence 0; CacheWindowView /
+    # CacheRetrievalView take b= for the others).
     @property
     def windows(self):
-        return self.caches
+        return [CacheWindowView(self, li) for li in range(self.n_layers)]
 
     @property
     def retrievals(self):
-        return self.caches
+        return [CacheRetrievalView(self, li) for li in range(self.n_layers)]
 
     def _layers(self):
         return self.model.model.layers
 
     def _dtype(self):
-        """Window storage dtype: the model's when bf16/fp16, else bf16 (the window kernels
-        read 16-bit K/V)."""
+        """Window storage dtype: the model's (bf16, fp16 or fp32)."""
         dt = next(self.model.parameters()).dtype
-        return dt if dt in (torch.bfloat16, torch.float16) else torch.bfloat16
+        return dt if dt in (torch.bfloat16, torch.float16, torch.float32) else torch.float32
+
+    @staticmethod
+    def _out_dtype(dt):
+        """Attention output dtype: bf16 for bf16 models, else fp32, rounded once to the model
+        dtype afterwards (the reference rounds its fp32 attention to the model dtype,
+        kvr_hook.py:280)."""
+        return torch.bfloat16 if dt == torch.bfloat16 else torch.float32
 
     def _rope(self, ref, positions):
         """cos, sin [B, L, d] for absolute positions [B, L] (model dtype, as HF)."""
@@ -97,8 +116,9 @@ class KVRHook:
         into the exact window and the 1-bit tile store as it is produced."""
         B, L = input_ids.shape
         dt = self._dtype()
+        extra = max(64, -(-self.reserve_tokens // self.tile) + 1)  # tiles the decode steps will add
         self.caches = [TileKVCache(B, self.n_kv, self.window_size, self.tile, self.transform, self.device, dt,
-                                   tile_cap=max(64, L // self.tile + 64)) for _ in range(self.n_layers)]
+                                   tile_cap=L // self.tile + extra) for _ in range(self.n_layers)]
         hooks = []
 
         def make(li):
@@ -144,8 +164,8 @@ class KVRHook:
             if self._step > 0:
                 self._update_stores(li, None, v[:, 0], k_rot)
             cache = self.caches[li]
-            top = self.top_k if (self._ret_weight > 0) else 0
-            attn = cache.attend(q_rot.contiguous(), top, out_dtype=torch.bfloat16)
+            top = self.top_k if (self._ret_weight > 0) else 0  # ret_weight <= 0: window only (kvr_hook.py:261)
+            attn = cache.attend(q_rot.contiguous(), top, out_dtype=self._out_dtype(hidden.dtype))
             proj = mod.o_proj(attn.reshape(B, 1, self.n_q * self.d_head).to(hidden.dtype))
             if self.num_denoise_steps > 0:
                 layer = self._layers()[li]
@@ -158,6 +178,12 @@ class KVRHook:
             new_attn[:, -1:, :] = proj
             return (new_attn,) + tuple(output[1:])
         return hook
+
+    def check(self):
+        """Synchronising status check of every layer (see the module docstring)."""
+        for c in self.caches:
+            if c is not None:
+                c.check()
 
     def register(self):
         for li, layer in enumerate(self._layers()):

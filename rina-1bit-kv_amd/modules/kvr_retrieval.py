@@ -165,17 +165,32 @@ class RetrievalIndex:
         out = _hip.gather_tiles(bits, scales, idx, self.tile, self.transform)  # [n_kv, k*T, d]
         return out.permute(1, 0, 2)
 
+    def _all_keys(self):
+        """Every stored key, decoded, post-RoPE, in position order: (n_stored, n_kv, d) fp32."""
+        keys = [self.tail_k]
+        if self.n_tiles:
+            idx = torch.arange(self.n_tiles, device=self.device, dtype=torch.int32).repeat(self.n_kv, 1)
+            keys.insert(0, self._tokens(self.kbits, self.kscale, idx))
+        return torch.cat(keys)
+
+    @torch.no_grad()
+    def _deq_k(self, kvh):
+        """Decoded keys of KV head kvh as pre-RoPE fp32 (n_stored, d) (kvr_retrieval.py:125-129).
+        The store holds post-RoPE keys, so they are rotated back: _rotary(_deq_k(h), positions)
+        gives the decoded post-RoPE keys, the pattern of scripts/evaluation/_diag_rank.py:76-77."""
+        k = self._all_keys()[:, kvh]
+        if self.cos is None:
+            return k
+        n = k.shape[0]
+        return _reverse_rotary(k, self.cos[:n].float(), self.sin[:n].float())
+
     @torch.no_grad()
     def compute_all_scores(self, q_post_rope):
         """Token-level cosine scores (n_stored, n_kv) on the decoded tokens (kvr_retrieval.py:265-289)."""
         n_q = q_post_rope.shape[0]
         g = n_q // self.n_kv
         q_avg = q_post_rope.float().view(self.n_kv, g, self.d_head).mean(dim=1)
-        keys = [self.tail_k]
-        if self.n_tiles:
-            idx = torch.arange(self.n_tiles, device=self.device, dtype=torch.int32).repeat(self.n_kv, 1)
-            keys.insert(0, self._tokens(self.kbits, self.kscale, idx))
-        k = torch.cat(keys)
+        k = self._all_keys()
         qn = q_avg / (q_avg.norm(dim=-1, keepdim=True) + 1e-8)
         kn = k / (k.norm(dim=-1, keepdim=True) + 1e-8)
         scores = torch.einsum('hd,thd->th', qn, kn)

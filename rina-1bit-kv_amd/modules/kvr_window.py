@@ -3,7 +3,7 @@ modules/kvr_window.py:9-69), attended exactly by the gfx950 window-attention ker
 
 Same constructor, attributes (k, v, pos, n, cap), append / batch_append ring semantics and
 attention() return convention as the reference.  Additions: `dtype` (fp16 as in the
-reference, or bf16) and `batch` (None keeps the reference's (cap, n_kv, d) layout; an int
+reference, bf16, or fp32) and `batch` (None keeps the reference's (cap, n_kv, d) layout; an int
 gives (batch, cap, n_kv, d) with per-call tensors carrying a leading batch dim).
 """
 from __future__ import annotations
@@ -19,8 +19,8 @@ class WindowBuffer:
     def __init__(self, n_kv, d_head, window_size=2048, device='cuda', dtype=torch.float16, batch=None):
         if d_head != 128:
             raise ValueError("the HIP kernels are built for head_dim 128")
-        if dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError("window dtype must be float16 or bfloat16")
+        if dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError("window dtype must be float16, bfloat16 or float32")
         self.n_kv = n_kv
         self.d_head = d_head
         self.cap = window_size

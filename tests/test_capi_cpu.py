@@ -81,8 +81,8 @@ def test_validation_errors_without_gpu(lib, H):
 
 
 def attn(lib, **kw):
-    a = dict(q=FAKE, qdt=0, B=1, Hq=32, Hkv=8, d=128, wk=FAKE, wv=FAKE, wdt=0, wl=64, sb=0, sh=8192,
-             st=128, kb=FAKE, vb=FAKE, ks=FAKE, vs=FAKE, ts=4, T=64, tf=0, idx=FAKE, k=2, out=FAKE,
+    a = dict(q=FAKE, qdt=0, B=1, Hq=32, Hkv=8, d=128, wk=FAKE, wv=FAKE, wdt=0, wl=64, w0=0, wc=0, sb=0,
+             sh=8192, st=128, kb=FAKE, vb=FAKE, ks=FAKE, vs=FAKE, ts=4, T=64, tf=0, idx=FAKE, k=2, out=FAKE,
              odt=2, ws=FAKE, wsb=0, s=None)
     a.update(kw)
     return lib.kvr_decode_attn(*a.values())
@@ -93,14 +93,61 @@ def test_decode_attn_validation(lib, H):
     assert attn(lib, Hq=8 * 17) == -5                  # g > 16 not built
     assert "g=17" in H.last_error()
     assert attn(lib, odt=1) == -1                      # fp16 output not offered
-    assert attn(lib, wdt=2) == -1                      # fp32 window not offered
+    assert attn(lib, wdt=3) == -1                      # unknown window dtype
+    assert attn(lib, wdt=2, st=126) == -2              # fp32 window: stride not a 16-byte multiple
+    assert attn(lib, wdt=2) == -3                      # fp32 window accepted (fails at the workspace)
     assert attn(lib, st=100) == -2                     # window stride not 16-byte multiple
     assert attn(lib, wk=FAKE_MIS) == -2
     assert attn(lib, k=2000) == -1
     assert attn(lib, idx=None) == -1                   # k > 0 needs idx
+    assert attn(lib, wc=32) == -1                      # win_len beyond the ring capacity
+    assert "ring" in H.last_error()
+    assert attn(lib, wc=128, w0=128) == -1             # ring start outside the ring
+    assert attn(lib, w0=3) == -1                       # a start without a ring
     assert attn(lib, wsb=10) == -3                     # workspace too small
     need = lib.kvr_decode_attn_workspace(1, 32, 8, 64, 2, 64)
     assert attn(lib, wsb=need, ws=ctypes.c_void_p(0x10040)) == -2   # workspace misaligned
+
+
+def step(lib, **kw):
+    a = dict(q=FAKE, qdt=0, B=1, Hq=32, Hkv=8, d=128, wk=FAKE, wv=FAKE, wdt=0, wl=63, w0=0, wc=128, sb=0,
+             sh=16384, st=128, kb=FAKE, vb=FAKE, ks=FAKE, vs=FAKE, kc=None, nt=8, ts=8, T=64, tf=0, lo=None,
+             hi=None, k=2, live=FAKE, out=FAKE, odt=2, idx=None, ws=FAKE, wsb=0, s=None)
+    a.update(kw)
+    return lib.kvr_decode_step(*a.values())
+
+
+def test_decode_step_live_validation(lib, H):
+    assert step(lib, live=FAKE_MIS) == -2              # live state misaligned
+    assert step(lib, wc=0) == -1                       # a live state needs a ring
+    assert step(lib, k=65, nt=100, ts=100) == -5       # beyond the one-launch step
+    assert "live state" in H.last_error()
+    assert step(lib, k=9) == -1                        # k > tile capacity
+    assert step(lib) == -3                             # otherwise valid: fails at the workspace
+
+
+def append(lib, **kw):
+    a = dict(k=FAKE, v=FAKE, ndt=0, B=1, Hkv=8, d=128, wk=FAKE, wv=FAKE, wdt=0, sb=0, sh=16384, st=128, W=64,
+             T=64, tf=0, kb=FAKE, vb=FAKE, ks=FAKE, vs=FAKE, kc=None, ts=8, state=FAKE, s=None)
+    a.update(kw)
+    return lib.kvr_cache_append(*a.values())
+
+
+def test_cache_append_validation(lib, H):
+    assert append(lib, W=32) == -1                     # W not a multiple of T
+    assert append(lib, W=0) == -1
+    assert append(lib, tf=2) == -1                     # the cache encodes Hadamard or DCT
+    assert append(lib, ndt=5) == -1
+    assert append(lib, st=100) == -2                   # window stride
+    assert append(lib, state=FAKE_MIS) == -2           # state alignment
+    assert append(lib, state=None) == -1
+    assert append(lib, ts=0) == -1                     # store pitch
+    assert append(lib, B=0) == 0                       # nothing to do
+
+
+def test_wait_limit_validation(lib):
+    assert lib.kvr_set_wait_limit(-1, 0) == -1
+    assert lib.kvr_set_wait_limit(0, 0) == 0           # restores the default
 
 
 def test_workspace_sizes(lib):

@@ -117,7 +117,7 @@ def test_hook_prefill_state_bit_exact(M):
     for li, c in enumerate(hook.caches):
         assert c.n_tiles == n_ret // T and c.n == L - n_ret
         k = kp[li]
-        assert torch.equal(c.win_k[:, :, :c.n], k[:, :, n_ret:])
+        assert torch.equal(c.window_tokens()[0], k[:, :, n_ret:])
         x = k[:, :, :n_ret].float().cpu().numpy().reshape(B * 2, n_ret, 128)
         rb, rs = O.encode(x, T, O.HADAMARD)
         assert np.array_equal(c.kbits[:, :c.n_tiles].cpu().numpy().view(np.uint64), rb)
@@ -154,7 +154,7 @@ def test_hook_decode_with_retrieval_runs_and_tracks_positions(M):
     c = hook.caches[0]
     n_ret = c.n_tiles * T
     ref = native_k_post(model, full[:, :n_stored])[0][:, :, n_ret:].float()
-    got = c.win_k[:, :, :c.n].float()
+    got = c.window_tokens()[0].float()
     assert ((got - ref).abs() <= 2 ** -6 * ref.abs() + 1e-3).all()
 
 
@@ -198,7 +198,8 @@ def test_cache_append_evict_matches_oracle(M, rng, tf):
     # evictions at n = W + T: 136 + 56 -> 2 tiles, then 128 + 44 -> n = 172
     assert (c.n_tiles, c.n) == (2, 172)
     nr = c.n_tiles * T
-    assert torch.equal(c.win_k[:, :, :c.n], k[:, :, nr:]) and torch.equal(c.win_v[:, :, :c.n], v[:, :, nr:])
+    wk, wv = c.window_tokens()
+    assert torch.equal(wk, k[:, :, nr:]) and torch.equal(wv, v[:, :, nr:])
     for bits, sc, x in ((c.kbits, c.kscale, k), (c.vbits, c.vscale, v)):
         xv = x[:, :, :nr].float().cpu().numpy().reshape(B * Hkv, nr, 128)
         if tf == O.HADAMARD:
@@ -223,8 +224,7 @@ def test_cache_append_evict_matches_oracle(M, rng, tf):
         assert np.array_equal(idx_out.cpu().numpy(), idx)
     else:
         idx = idx_out.cpu().numpy()  # near ties may order differently under the DCT tolerance
-    ref = O.decode_attention(qn, c.win_k.float().cpu().numpy(), c.win_v.float().cpu().numpy(), kb, vb, ks, vs,
-                             idx, tf, win_len=c.n)
+    ref = O.decode_attention(qn, wk.float().cpu().numpy(), wv.float().cpu().numpy(), kb, vb, ks, vs, idx, tf)
     assert np.abs(out.cpu().numpy() - ref).max() < 1e-5
 
 
@@ -351,3 +351,213 @@ def test_retrieval_index_single_appends(M, rng):
     assert ri.n_tiles == 1 and ri.tail_k.shape[0] == 6 and ri.n_stored == 70
     rb, rs = O.encode(k[:64].permute(1, 0, 2).cpu().numpy(), 64, O.HADAMARD)  # no rotary tables
     assert np.array_equal(ri.kbits[:, :1].cpu().numpy().view(np.uint64), rb)
+
+
+# ----------------------------------------------------------------------------- retrieval active
+
+def spy_attend(cache, log):
+    """Record layer state and output of every attend call of one TileKVCache (after the call,
+    synchronised): q, the window in token order, the stored tiles, and the output."""
+    orig = cache.attend
+
+    def spy(q, top_k_tokens, **kw):
+        out = orig(q, top_k_tokens, **kw)
+        torch.cuda.synchronize()
+        wk, wv = cache.window_tokens()
+        nt = cache.n_tiles
+        log.append(dict(q=q.float().cpu().numpy(), wk=wk.float().cpu().numpy(), wv=wv.float().cpu().numpy(),
+                        kb=cache.kbits[:, :nt].cpu().numpy().view(np.uint64),
+                        vb=cache.vbits[:, :nt].cpu().numpy().view(np.uint64),
+                        ks=cache.kscale[:, :nt].cpu().numpy(), vs=cache.vscale[:, :nt].cpu().numpy(),
+                        k=cache.k_tiles(top_k_tokens), out=out.float().cpu().numpy(), odt=out.dtype))
+        return out
+    cache.attend = spy
+
+
+def check_logged(log, Hkv, tf=O.HADAMARD):
+    """Each logged attend call against the oracle pipeline on the same stored state."""
+    assert log
+    for i, r in enumerate(log):
+        qbar, _ = O.query_prep(r["q"], Hkv, tf)
+        idx = O.topk_tiles(O.score_tiles(qbar.reshape(-1, 128), r["kb"]), r["k"]) if r["k"] else None
+        ref = O.decode_attention(r["q"], r["wk"], r["wv"], r["kb"], r["vb"], r["ks"], r["vs"], idx, tf)
+        if r["odt"] == torch.float32:
+            err = np.abs(r["out"] - ref).max()
+            assert err <= 1e-5, (i, err)
+        else:
+            excess = (np.abs(r["out"] - ref) - (2e-3 + np.abs(ref) * 2.0 ** -8)).max()
+            assert excess <= 0, (i, excess)
+
+
+def test_hook_retrieval_active_matches_oracle(M):
+    """Prompt longer than the window, decode across an eviction: layer 0's attention output at
+    every step equals the oracle pipeline (scores, top-k, joint softmax) on the cache's own
+    stored state, with retrieval active (tiles selected every step)."""
+    say("[hook/retrieval active] layer 0 vs oracle every step")
+    model = tiny_llama()
+    B, L, W, T, steps = 1, 300, 128, 64, 40
+    full = token_ids(B, L + steps, seed=21)
+    hook = M.KVRHook(model, window_size=W, top_k=128, tile=T, num_denoise_steps=0)
+    hook.prefill(full[:, :L])
+    log = []
+    spy_attend(hook.caches[0], log)
+    hook.register()
+    try:
+        for s in range(steps):
+            p = L - 1 + s
+            with torch.no_grad():
+                model(full[:, p:p + 1], use_cache=False)
+            hook._step += 1
+            hook._context_len += 1
+    finally:
+        hook.remove()
+    hook.check()
+    assert all(r["k"] == 2 for r in log) and len(log) == steps
+    assert hook.caches[0].n_tiles == 3  # 2 from the prefill, 1 evicted during decode
+    check_logged(log, 2)
+
+
+def test_hook_ret_weight_zero_is_window_only(M):
+    """ret_weight <= 0 skips retrieval (kvr_hook.py:261): with tiles stored, the attention is
+    the window-only softmax."""
+    say("[hook/ret_weight=0]")
+    model = tiny_llama()
+    B, L, W, T = 1, 300, 128, 64
+    full = token_ids(B, L + 3, seed=22)
+    hook = M.KVRHook(model, window_size=W, top_k=128, ret_weight=0.0, tile=T, num_denoise_steps=0)
+    hook.prefill(full[:, :L])
+    log = []
+    spy_attend(hook.caches[0], log)
+    hook.register()
+    try:
+        for s in range(3):
+            with torch.no_grad():
+                model(full[:, L - 1 + s:L + s], use_cache=False)
+            hook._step += 1
+            hook._context_len += 1
+    finally:
+        hook.remove()
+    assert hook.caches[0].n_tiles == 2 and all(r["k"] == 0 for r in log)
+    check_logged(log, 2)
+
+
+def test_hook_fp16_model_within_window(M):
+    """fp16 model: attention computed in fp32 and rounded once to fp16; logits equal the
+    native model's within the same bar as bf16."""
+    say("[hook/fp16 model]")
+    model = tiny_llama(dtype=torch.float16)
+    B, L, steps = 1, 50, 4
+    full = token_ids(B, L + steps, seed=23)
+    with torch.no_grad():
+        native = model(full, use_cache=False).logits.float()
+    hook = M.KVRHook(model, window_size=256, top_k=128, num_denoise_steps=0)
+    hook.prefill(full[:, :L])
+    assert hook.caches[0].dtype == torch.float16
+    hook.register()
+    try:
+        for s in range(steps):
+            p = L - 1 + s
+            with torch.no_grad():
+                got = model(full[:, p:p + 1], use_cache=False).logits[:, -1].float()
+            hook._step += 1
+            hook._context_len += 1
+            assert rel_err(got, native[:, p]) < 2e-2
+    finally:
+        hook.remove()
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_generator_graph_equals_eager_with_retrieval(M, B):
+    """KVRGenerator with retrieval active (prompt > window) across evictions: the graph path
+    (one captured token, replayed, with the caller's eager work between replays) gives the
+    same logits as the eager path at every step, and leaves the same cache state (two
+    evictions happen inside the replays)."""
+    say(f"[generator/graph vs eager] B={B}")
+    model = tiny_llama()
+    L, W, T, steps = 300, 128, 64, 90
+    full = token_ids(B, L + steps, seed=24)
+    runs = []
+    for graphs in (False, True):
+        gen = M.KVRGenerator(model, window_size=W, top_k=128, tile=T, graphs=graphs)
+        gen.prefill(full[:, :L])
+        log = []
+        logits = []
+        for s in range(steps):
+            p = L - 1 + s
+            gen.step(full[:, p:p + 1], do_sample=False)
+            logits.append(gen.last_logits.clone())
+        gen.kvr.check()
+        runs.append((logits, gen, log))
+    (le, ge, _), (lg, gg, logg) = runs
+    assert gg.graph_captures >= 1 and gg.graph_replays == steps - 1, (gg.graph_captures, gg.graph_replays)
+    assert ge.graph_replays == 0
+    for s in range(steps):
+        err = rel_err(lg[s], le[s])
+        assert err <= 1e-6, (s, err)
+    ce, cg = ge.kvr.caches[0], gg.kvr.caches[0]
+    assert (ce.n, ce.start, ce.n_tiles) == (cg.n, cg.start, cg.n_tiles)
+    assert cg.n_tiles == 4 and cg.start == 2 * T  # two evictions, both inside the replays
+    st = cg.state.cpu().numpy()
+    assert (st[:, :3] == np.array([cg.n, cg.start, cg.n_tiles])).all() and not st[:, 3].any()
+    assert torch.equal(ce.kbits, cg.kbits) and torch.equal(ce.win_k, cg.win_k)
+
+
+def test_generator_layer0_matches_oracle(M):
+    """Eager generator with retrieval active: layer 0's attention vs the oracle every step."""
+    say("[generator/layer 0 vs oracle]")
+    model = tiny_llama()
+    B, L, W, T, steps = 1, 300, 128, 64, 30
+    full = token_ids(B, L + steps, seed=25)
+    gen = M.KVRGenerator(model, window_size=W, top_k=128, tile=T, graphs=False)
+    gen.prefill(full[:, :L])
+    log = []
+    spy_attend(gen.kvr.caches[0], log)
+    for s in range(steps):
+        gen.step(full[:, L - 1 + s:L + s], do_sample=False)
+    check_logged(log, 2)
+
+
+# ----------------------------------------------------------------------------- per-layer views
+
+def test_hook_views_reference_calling_pattern(M):
+    """hook.retrievals[li] / hook.windows[li] used as scripts/evaluation/_diag_rank.py:59-83
+    uses them: n_stored, compute_all_scores on a GQA-averaged query (values against the
+    oracle's dequantise -> cosine, kvr_retrieval.py:265-289), _rotary(_deq_k(h), positions)
+    giving the decoded post-RoPE keys, chunk scores, retrieve_topk, attribute writes."""
+    say("[hook views] _diag_rank pattern")
+    model = tiny_llama()
+    B, L, W, T = 1, 300, 128, 64
+    ids = token_ids(B, L, seed=26)
+    hook = M.KVRHook(model, window_size=W, top_k=128, tile=T)
+    hook.prefill(ids)
+    li = 1
+    ret = hook.retrievals[li]
+    win = hook.windows[li]
+    c = hook.caches[li]
+    nr = ret.n_stored
+    assert nr == 2 * T and win.n == L - nr and win.pos == L and win.cap == W + T
+    kp = native_k_post(model, ids)[li][0]                                   # [Hkv, L, 128]
+    assert torch.equal(win.k.permute(1, 0, 2), kp[:, nr:])
+    g = torch.Generator().manual_seed(5)
+    q_avg = torch.randn(2, 128, generator=g).to(DEV)                        # GQA-averaged, one per KV head
+    sc = ret.compute_all_scores(q_avg)
+    assert sc.shape == (nr, 2)
+    kb = c.kbits[:, :2].cpu().numpy().view(np.uint64)
+    ks = c.kscale[:, :2].cpu().numpy()
+    for h in range(2):
+        keys = O.dequantize_original(kb[h], ks[h], O.HADAMARD).reshape(-1, 128)
+        qv = q_avg[h].double().cpu().numpy()
+        ref = (keys @ (qv / (np.linalg.norm(qv) + 1e-8))) / (np.linalg.norm(keys, axis=-1) + 1e-8)
+        assert np.abs(sc[:, h].double().cpu().numpy() - ref).max() < 1e-5
+        kpre = ret._deq_k(h)
+        kpost = ret._rotary(kpre[:, None], torch.arange(nr, device=DEV))[:, 0]
+        assert (kpost.double().cpu().numpy() - keys).__abs__().max() < 1e-4 * np.abs(keys).max()
+    chunk = ret.compute_chunk_scores(torch.randn(8, 128, generator=g).to(DEV))
+    assert chunk.shape == (2, 2)
+    Kr, Vr = ret.retrieve_topk(torch.randn(8, 128, generator=g).to(DEV), n_q=8)
+    assert Kr.shape == (2 * T, 2, 128) and Kr.dtype == torch.float32 and Vr.dtype == torch.float16
+    ret.chunk_size = 0
+    ret.attractors = None
+    ret.n_attractors = 256  # accepted, no effect
+    out = win.attention(torch.randn(8, 128, generator=g).to(DEV))
+    assert out.shape == (8, 128) and torch.isfinite(out).all()

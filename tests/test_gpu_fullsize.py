@@ -1,10 +1,14 @@
 """GPU parity at the benchmark configurations' full sizes, through the C ABI.
 
 configs[2] (B=16, GQA 32/8, 32768-token context, bf16 window 1024, Hadamard tiles of 64,
-top-32) and configs[4] (B=4, GQA 28/4, 131072-token context, window 2048, DCT tiles of 128,
-top-64): the one-launch decode step against the CPU oracle on the same stored inputs --
-every segment's selected tiles, and every head's output within the attention tolerance --
-scoring from the K store's per-tile channel counts (the product path) and from the bits.
+top-32), configs[3]'s per-layer decode step (B=1, GQA 32/8, 992 tiles, window 2048, top-64
+tiles of 64: the single-wave selection at its 64-entry limit) and configs[4] (B=4, GQA 28/4,
+131072-token context, window 2048, DCT tiles of 128, top-64): the one-launch decode step
+against the CPU oracle on the same stored inputs -- every segment's selected tiles, and
+every head's output within the attention tolerance -- scoring from the K store's per-tile
+channel counts (the product path) and from the bits.  configs[3] also through the
+product's TileKVCache (ring window, live device state), and configs[0] end to end: fp32
+K/V with planted query-aligned keys, fp32 window, fp32 output.
 Encoders at full size (configs[1]: 32 layers x 8 KV heads x 16384 tokens; one configs[4]
 layer: 4 x 4 x 131072 tokens): sampled segments bit-exact against the oracle codec
 (Hadamard from the input, DCT given the kernel's own rotation, which is held to 1e-6 of
@@ -71,6 +75,7 @@ def topk_agree(ig, iref, sref, k, exact):
 @pytest.mark.parametrize(
     "cfg,B,Hq,Hkv,N,W,T,k,tf",
     [("configs[2]", 16, 32, 8, 32768, 1024, 64, 32, O.HADAMARD),
+     ("configs[3]", 1, 32, 8, 65536, 2048, 64, 64, O.HADAMARD),
      ("configs[4]", 4, 28, 4, 131072, 2048, 128, 64, O.DCT)])
 @pytest.mark.parametrize("odt,use_counts", [(torch.bfloat16, True), (torch.float32, True), (torch.float32, False)])
 def test_decode_step_full_size(H, cfg, B, Hq, Hkv, N, W, T, k, tf, odt, use_counts):
@@ -137,3 +142,89 @@ def test_encode_full_size_configs4_dct(H):
         gb = bits.view(16, -1)[s].cpu().numpy().view(np.uint64).reshape(1, -1)[:, :rb.size].reshape(rb.shape)
         assert np.array_equal(gb, rb), s
         assert np.array_equal(scales[s, :128].cpu().numpy().view(np.uint16), rsc.view(np.uint16).reshape(-1)), s
+
+
+def test_configs3_through_tile_cache(H):
+    """configs[3]'s decode step as the generator runs it: a 65536-token prompt loaded into a
+    TileKVCache (992 tiles + a 2048..2111-token ring window), 70 appended tokens (one
+    eviction, in the ring), then attention from the live device state -- against the oracle
+    on the cache's own stored state."""
+    import modules
+    say("[fullsize/configs[3] cache] B=1 GQA 32/8 65536 + 70 tokens, W=2048, T=64, top-64 tiles")
+    B, Hq, Hkv, L, W, T, k = 1, 32, 8, 65536, 2048, 64, 64
+    c = modules.TileKVCache(B, Hkv, W, T, H.HADAMARD, DEV, torch.bfloat16, tile_cap=L // T + 64)
+    K = gen_kv((B, Hkv, L + 70, 128), 30)
+    V = gen_kv((B, Hkv, L + 70, 128), 31, outliers=False)
+    c.load_prompt(K[:, :, :L], V[:, :, :L])
+    for t in range(L, L + 70):
+        c.append(K[:, :, t], V[:, :, t])
+    assert (c.n_tiles, c.n, c.start) == (993, 2054, 64)  # one eviction after 64 appends, then 6 more
+    q = gen_kv((B, Hq, 128), 32, outliers=False)
+    idx = torch.empty((B * Hkv, k), dtype=torch.int32, device=DEV)
+    out = c.attend(q, k * T, out_dtype=torch.float32, idx_out=idx)
+    c.check()
+    nt = c.n_tiles
+    kbn, vbn = u64(c.kbits[:, :nt]), u64(c.vbits[:, :nt])
+    ksn, vsn = c.kscale[:, :nt].cpu().numpy(), c.vscale[:, :nt].cpu().numpy()
+    rb, _ = O.encode(K[:, :, :nt * T].float().cpu().numpy().reshape(B * Hkv, nt * T, 128)[:, -2 * T:], T, O.HADAMARD)
+    assert np.array_equal(kbn[:, -2:], rb)  # the last prefill tile and the one the append encoded
+    qn = q.float().cpu().numpy()
+    qbar, _ = O.query_prep(qn, Hkv, O.HADAMARD)
+    iref = O.topk_tiles(O.score_tiles(qbar.reshape(-1, 128), kbn), k)
+    assert np.array_equal(idx.cpu().numpy(), iref)
+    wk, wv = c.window_tokens()
+    assert torch.equal(wk, K[:, :, nt * T:L + 70])
+    ref = O.decode_attention(qn, wk.float().cpu().numpy(), wv.float().cpu().numpy(), kbn, vbn, ksn, vsn, iref,
+                             O.HADAMARD)
+    check_out(out, ref, "configs[3] cache")
+
+
+def test_configs0_end_to_end_fp32(H):
+    """one layer, batch 1, GQA 32/8, 4096-token context in fp32, K, V ~ N(0,1) x a
+    per-(head, channel) log-normal scale (sigma 1, independent for K and V, seed 0), q ~
+    N(0,1), 4 keys at seeded positions set to (0.8 qhat_h + 0.2 noise) x the head's median key
+    norm; Hadamard-128, 64-token tiles, the last 512 tokens as an fp32 window, top-8 tiles.
+    fp32 end to end: bits and scales from the fp32 keys, top-8 index-exact and the output
+    within 1e-5 x max(1, max |ref|) of the float64 oracle; planted-tile recall is reported,
+    not gated."""
+    say("[configs[0]] fp32 B=1 GQA 32/8 N=4096 W=512 T=64 top-8, 4 planted keys")
+    B, Hq, Hkv, N, W, T, k = 1, 32, 8, 4096, 512, 64, 8
+    g = np.random.default_rng(0)
+    K = g.standard_normal((B, Hkv, N, 128)) * np.exp(g.standard_normal((1, Hkv, 1, 128)))
+    V = g.standard_normal((B, Hkv, N, 128)) * np.exp(g.standard_normal((1, Hkv, 1, 128)))
+    q = g.standard_normal((B, Hq, 128))
+    qbar = q.reshape(B, Hkv, Hq // Hkv, 128).mean(2)
+    qhat = qbar / np.linalg.norm(qbar, axis=-1, keepdims=True)
+    n_ret = N - W
+    pos = g.choice(n_ret, size=4, replace=False)
+    rho = np.median(np.linalg.norm(K[0], axis=-1), axis=-1)  # [Hkv]
+    for p in pos:
+        noise = g.standard_normal((Hkv, 128))
+        noise /= np.linalg.norm(noise, axis=-1, keepdims=True)
+        K[0, :, p] = (0.8 * qhat[0] + 0.2 * noise) * rho[:, None]
+    K, V, q = K.astype(np.float32), V.astype(np.float32), q.astype(np.float32)
+    Kd, Vd = torch.from_numpy(K).to(DEV), torch.from_numpy(V).to(DEV)
+    counts = H.alloc_counts(B * Hkv, n_ret // T, DEV)
+    kb, ks = H.encode_tiles(Kd[:, :, :n_ret], T, H.HADAMARD, counts=counts)
+    vb, vs = H.encode_tiles(Vd[:, :, :n_ret], T, H.HADAMARD)
+    wk, wv = Kd[:, :, n_ret:].contiguous(), Vd[:, :, n_ret:].contiguous()
+    idx = torch.empty((B * Hkv, k), dtype=torch.int32, device=DEV)
+    out = H.decode_step(torch.from_numpy(q).to(DEV), wk, wv, W, kb, vb, ks, vs, n_ret // T, T, H.HADAMARD, k,
+                        out_dtype=torch.float32, idx_out=idx, kcounts=counts)
+    torch.cuda.synchronize()
+    rb, rs = O.encode(K[:, :, :n_ret].reshape(B * Hkv, n_ret, 128), T, O.HADAMARD)
+    assert np.array_equal(u64(kb), rb) and np.array_equal(ks.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    qb, _ = O.query_prep(q, Hkv, O.HADAMARD)
+    iref = O.topk_tiles(O.score_tiles(qb.reshape(-1, 128), rb), k)
+    ig = idx.cpu().numpy()
+    assert np.array_equal(ig, iref)
+    ref = O.decode_attention(q, K[:, :, n_ret:], V[:, :, n_ret:], rb, u64(vb), rs, vs.cpu().numpy(), iref,
+                             O.HADAMARD)
+    err = float(np.abs(out.cpu().numpy() - ref).max())
+    scale = max(1.0, float(np.abs(ref).max()))
+    # V's per-channel log-normal scale puts outputs at O(10) (max |ref| ~26 here): the fp32 bar
+    # of 1e-5 is applied relative to the output scale (measured: ~5e-7 relative, the window's
+    # fp32 accumulation over 512 tokens; the retrieved part ~4e-7)
+    assert err <= 1e-5 * scale, (err, scale)
+    hits = sum(int(p // T in ig[h]) for p in pos for h in range(Hkv))
+    say(f"  max-abs {err:.2e} (max |ref| {scale:.1f}); planted-tile recall {hits}/{4 * Hkv}")
