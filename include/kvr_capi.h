@@ -172,6 +172,32 @@ int kvr_decode_step(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int 
                     const int32_t* live_state, void* out, int out_dtype, int32_t* idx_out,
                     void* workspace, size_t ws_bytes, kvr_stream_t stream);
 
+/* Scratch the allocation-free decode step holds per GPU (bytes). */
+#define KVR_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/*
+ * kvr_decode_step without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments (minus workspace, ws_bytes), semantics and
+ * results as kvr_decode_step; its scratch is a KVR_NOALLOC_SCRATCH_BYTES device array
+ * of the library, one per GPU, held until the process ends, zeroed on the first call
+ * on each device (which must not be under graph capture).  Sizes whose workspace
+ * (kvr_decode_step_workspace) exceeds it are rejected with KVR_ERR_WORKSPACE.  The
+ * function calls no hipMalloc / hipFree.  Calls that overlap on one GPU share that
+ * scratch and race: the caller serialises them.
+ * Replaces: nothing in the reference -- an addition for the callers that cannot
+ *           allocate (see above).
+ */
+int kvr_decode_step_noalloc(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
+                            const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
+                            int64_t win_start, int64_t win_cap, int64_t win_stride_b,
+                            int64_t win_stride_h, int64_t win_stride_t, const uint64_t* kbits,
+                            const uint64_t* vbits, const uint16_t* kscale, const uint16_t* vscale,
+                            const uint8_t* kcounts, int64_t n_tiles, int64_t tile_stride, int T,
+                            int transform, const int32_t* excl_lo, const int32_t* excl_hi, int k,
+                            const int32_t* live_state, void* out, int out_dtype, int32_t* idx_out,
+                            kvr_stream_t stream);
+
 /*
  * Append one token per segment to a per-layer cache: a ring window of W + T slots
  * (window layout as in kvr_decode_attn, any of bf16 / fp16 / fp32) plus the

@@ -300,7 +300,7 @@ int decode_step_impl(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int
                      int64_t n_tiles, int64_t tile_stride, int T, int transform,
                      const int32_t* excl_lo, const int32_t* excl_hi, int k, const int32_t* live_state,
                      void* out, int out_dtype, int32_t* idx_out, void* workspace, size_t ws_bytes,
-                     hipStream_t stream) {
+                     hipStream_t stream, bool launch) {
   if (n_tiles < 0) return fail(KVR_ERR_INVALID, "n_tiles < 0");
   if (n_tiles == 0) k = 0;
   if (k > n_tiles) return fail(KVR_ERR_INVALID, "k=%d > n_tiles=%lld", k, (long long)n_tiles);
@@ -322,6 +322,11 @@ int decode_step_impl(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int
   if (B == 0) return KVR_OK;
   const int64_t nt = (k > 0) ? n_tiles : 0;
   const StepLayout W = step_layout(B, Hq, Hkv, win_len, nt, k, T);
+  if (!launch) {
+    if (ws_bytes < W.total)
+      return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu available", W.total, ws_bytes);
+    return KVR_OK;
+  }
   if (!workspace || ws_bytes < W.total)
     return fail(KVR_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", W.total,
                 workspace ? ws_bytes : (size_t)0);

@@ -91,7 +91,8 @@ struct AppendLaunch {
 hipError_t launch_append(const AppendLaunch& L, hipStream_t s);
 
 // Decode-step entry point shared by kvr_decode_step and the allocation-free variant:
-// validates, lays out the workspace and launches.
+// validates, lays out the workspace and launches (launch == false: validation only, the
+// workspace pointer unchecked and only ws_bytes compared with the need).
 int decode_step_impl(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int d,
                      const void* win_k, const void* win_v, int win_dtype, int64_t win_len,
                      int64_t win_start, int64_t win_cap, int64_t win_stride_b, int64_t win_stride_h,
@@ -100,7 +101,7 @@ int decode_step_impl(const void* q, int q_dtype, int64_t B, int Hq, int Hkv, int
                      int64_t n_tiles, int64_t tile_stride, int T, int transform,
                      const int32_t* excl_lo, const int32_t* excl_hi, int k, const int32_t* live_state,
                      void* out, int out_dtype, int32_t* idx_out, void* workspace, size_t ws_bytes,
-                     hipStream_t stream);
+                     hipStream_t stream, bool launch = true);
 // Workspace bytes decode_step_impl needs (0 for invalid sizes).
 size_t decode_step_workspace_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int64_t n_tiles, int k, int T);
 // Sets the thread-local error message; returns code.

@@ -44,6 +44,8 @@ SIGNATURES = {
     "kvr_cache_append": (_I, [_P, _P, _I, _L, _I, _I, _P, _P, _I, _L, _L, _L, _L, _I, _I, _P, _P, _P, _P, _P,
                               _L, _P, _P]),
     "kvr_set_wait_limit": (_I, [_I, _I]),
+    "kvr_decode_step_noalloc": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P,
+                                     _P, _L, _L, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P]),
 }
 
 _lib = None
@@ -258,6 +260,33 @@ def decode_step(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles,
                                _ptr(live_state), _ptr(out), _DT[out.dtype], _ptr(idx_out), _ptr(workspace),
                                workspace.numel(), _stream())
     check(rc, "kvr_decode_step")
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # KVR_NOALLOC_SCRATCH_BYTES
+
+
+def decode_step_noalloc(q, win_k, win_v, win_len, kbits, vbits, kscale, vscale, n_tiles, T, transform, k,
+                        excl_lo=None, excl_hi=None, out_dtype=torch.bfloat16, out=None, idx_out=None,
+                        kcounts=None, win_start=0, win_cap=0, live_state=None):
+    """decode_step through kvr_decode_step_noalloc: no workspace (the library's per-GPU
+    scratch); the output (and idx_out) are the caller's."""
+    _require_gpu(q)
+    q = q.contiguous()
+    B, Hq, _ = q.shape
+    Hkv = win_k.shape[1] if win_k is not None else kbits.shape[0] // B
+    if live_state is not None:
+        _check_state(live_state, B * Hkv)
+    wk, wv, wdt, wl, w0, wc, sb, sh, st = _window_args(win_k, win_v, win_len, win_start, win_cap)
+    if out is None:
+        out = torch.empty((B, Hq, 128), dtype=out_dtype, device=q.device)
+    tile_stride = kbits.shape[1] if kbits is not None else 1
+    rc = lib().kvr_decode_step_noalloc(_ptr(q), _DT[q.dtype], B, Hq, Hkv, 128, _ptr(wk), _ptr(wv), wdt, wl, w0, wc,
+                                       sb, sh, st, _ptr(kbits), _ptr(vbits), _ptr(kscale), _ptr(vscale),
+                                       _ptr(kcounts), n_tiles, tile_stride, T, transform, _ptr(excl_lo),
+                                       _ptr(excl_hi), k, _ptr(live_state), _ptr(out), _DT[out.dtype], _ptr(idx_out),
+                                       _stream())
+    check(rc, "kvr_decode_step_noalloc")
     return out
 
 
