@@ -4,15 +4,19 @@ Default workload = BASELINE.json configs[2] ("decode32k"): one layer, batch 16, 
 context, GQA 32/8, head_dim 128, bf16 window of the last 1024 tokens, the other 31744 tokens
 pre-encoded to 1-bit tiles of 64 (Hadamard-128, sigma-delta), top-32 tiles per KV head.
 A step = one call of kvr_decode_step (query prep -> tile scores -> top-k -> fused window +
-retrieved-tile attention) over the batch, inputs resident in HBM.  value = decode tokens/s
-for that layer (B / step time).
+retrieved-tile attention) over the batch, inputs resident in HBM: the steps rotate over
+--layers copies of the layer's stores (more than the 256 MB last-level cache holds), so each
+step reads its layer from HBM as in a multi-layer decode.  value = decode tokens/s for that
+layer (B / step time).  The same step re-reading one layer (MALL-resident) is in extra.
 
 Also reported: encode GB/s at configs[1] (32 layers x 8 KV heads x 16384 tokens, K and V),
-the HBM roofline of the decode step, and the CPU oracle timed on a bounded sample.
+configs[4]'s decode step, configs[3] end to end (tokens/s of greedy decode on a random-init
+Llama-3-8B-architecture model with a 64k prompt), the HBM roofline of the decode step, and
+the CPU oracle on the host cores (1 thread and the box's 16).
 Synthetic data only (no checkpoints): K = N(0,1) * log-normal(sigma=1) per-channel scales with
 RoPE (base 500000) applied, V = N(0,1), q = N(0,1), 16 planted query-aligned keys per sequence.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-encode]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-encode] [--no-e2e]
        python bench.py --copy-calibration   (plain copy kernel for rocprof counter scaling)
 """
 import argparse
@@ -86,7 +90,7 @@ def plant_keys(K, q, n_plant, n_ret, Hkv, seed, device):
 
 class DecodeWorkload:
     def __init__(self, B=16, Hq=32, Hkv=8, N=32768, W=1024, T=64, k=32, transform=H.HADAMARD,
-                 device="cuda", seed=0, counts=True):
+                 device="cuda", seed=0, counts=True, keep_keys=False):
         self.B, self.Hq, self.Hkv, self.N, self.W, self.T, self.k = B, Hq, Hkv, N, W, T, k
         self.transform = transform
         n_ret = (N - W) // T * T
@@ -102,6 +106,7 @@ class DecodeWorkload:
         self.vbits, self.vscale = H.encode_tiles(V[:, :, :n_ret], T, transform)
         self.win_k = K[:, :, n_ret:].contiguous()
         self.win_v = V[:, :, n_ret:].contiguous()
+        self.K_ret = K[:, :, :n_ret] if keep_keys else None  # for the exact-tile-mean recall diagnostic
         del K, V
         self.out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=device)
         self.idx = torch.empty((B * Hkv, k), dtype=torch.int32, device=device)
@@ -144,6 +149,23 @@ class DecodeWorkload:
         qo = 2 * self.B * self.Hq * D * 2
         comp = BH * (scan + sel)
         return comp + BH * win + qo, comp
+
+    def planted_recall_exact(self):
+        """Recall of the planted keys' tiles when tiles are scored with their exact fp32 mean
+        keys (no 1-bit codec): separates the codec's loss from the dilution of a planted key
+        in its tile's mean.  A diagnostic in torch on the stored bf16 keys."""
+        B, Hkv, T, n = self.B, self.Hkv, self.T, self.n_tiles
+        qbar = self.q.float().view(B, Hkv, self.Hq // Hkv, D).mean(2)
+        hit = tot = 0
+        for b in range(B):
+            means = self.K_ret[b].float().view(Hkv, n, T, D).mean(2)              # [Hkv, n, D]
+            cos = (means @ qbar[b][:, :, None])[..., 0] / (means.norm(dim=-1) * qbar[b].norm(dim=-1)[:, None] + 1e-8)
+            top = cos.topk(self.k, dim=-1).indices.cpu()
+            for t in (self.planted[b] // T).tolist():
+                for h in range(Hkv):
+                    tot += 1
+                    hit += int(t in top[h].tolist())
+        return hit / max(tot, 1)
 
     def planted_recall(self):
         idx = self.idx.view(self.B, self.Hkv, self.k).cpu()
@@ -232,7 +254,8 @@ def e2e_benchmark(n_prompt=65536, n_new=128, n_layers=32):
     uniform random token ids (seed 0).  The prompt goes through the model once (SDPA attention;
     the materialising math backend is switched off so a 64 k prompt never builds N x N scores)
     with every layer's K/V encoded as it is produced; then n_new greedy steps, timed with events
-    as one async sequence (the generated ids stay on the device)."""
+    as one async sequence (the generated ids stay on the device): each token one replay of the
+    captured per-token graph, then the same number of steps eagerly for comparison."""
     from transformers import LlamaConfig, LlamaForCausalLM
     from modules import KVRGenerator
     torch.backends.cuda.enable_math_sdp(False)
@@ -249,7 +272,7 @@ def e2e_benchmark(n_prompt=65536, n_new=128, n_layers=32):
     finally:
         torch.set_default_dtype(prev)
     ids = torch.randint(0, cfg.vocab_size, (1, n_prompt), generator=torch.Generator().manual_seed(0)).cuda()
-    gen = KVRGenerator(model, window_size=2048, top_k=64 * 64)
+    gen = KVRGenerator(model, window_size=2048, top_k=64 * 64, reserve_tokens=2 * n_new + 64)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     gen.prefill(ids)
@@ -258,58 +281,180 @@ def e2e_benchmark(n_prompt=65536, n_new=128, n_layers=32):
     log(f"  e2e prefill of {n_prompt} tokens: {prefill_s:.2f} s")
     gen.step(ids[:, -1:], do_sample=False)  # step 0 (its token is already stored), untimed
     for _ in range(2):
-        gen.step(do_sample=False)
+        gen.step(do_sample=False)            # the first appending step captures the graph
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(n_new):
-        gen.step(do_sample=False)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1)
+
+    def timed_steps():
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n_new):
+            gen.step(do_sample=False)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    r0 = gen.graph_replays
+    ms = timed_steps()
+    replays = gen.graph_replays - r0
+    gen.use_graphs = False                   # the same steps without the graph, for comparison
+    ms_eager = timed_steps()
+    gen.kvr.check()
     res = {"e2e_config": f"configs[3]: random-init Llama-3-8B architecture ({n_layers} layers), bf16, batch 1, "
                          f"{n_prompt}-token random prompt, window 2048, top-64 tiles of 64",
            "e2e_prefill_s": round(prefill_s, 3), "e2e_new_tokens": n_new,
            "e2e_decode_ms_per_token": round(ms / n_new, 4),
            "e2e_decode_tokens_per_s": round(n_new / (ms / 1e3), 2),
+           "e2e_graph_replays": replays,
+           "e2e_decode_tokens_per_s_eager": round(n_new / (ms_eager / 1e3), 2),
            "e2e_context_at_end": gen.kvr._context_len}
     del gen, model
     torch.cuda.empty_cache()
     return res
 
 
-def cpu_baseline(wl, min_seconds=12.0):
-    """The numpy oracle on one host core, repeating the whole-batch decode step (query prep,
-    scoring of every tile, top-k, float64 attention; all B sequences) until min_seconds of
-    CPU work have been timed.  Inputs are copied to host memory first (not timed)."""
-    from threadpoolctl import threadpool_limits
+# ----------------------------------------------------------------------------- CPU baseline
+
+_CPU = {}  # the current CPU workload, inherited by forked pool workers
+
+
+def _cpu_segments(segs):
+    """The numpy oracle's decode step for segments segs (one (sequence, KV head) each): query
+    prep, scores of all its tiles, top-k, float64 attention over its window + selected tiles."""
     from oracle import kvr_oracle as O
-    Hkv = wl.Hkv
-    q = wl.q.float().cpu().numpy()
-    wk = wl.win_k.float().cpu().numpy()
-    wv = wl.win_v.float().cpu().numpy()
-    kb = wl.kbits.cpu().numpy().view(np.uint64)
-    vb = wl.vbits.cpu().numpy().view(np.uint64)
-    ks = wl.kscale.cpu().numpy()
-    vs = wl.vscale.cpu().numpy()
-    reps = 0
-    with threadpool_limits(limits=1):
+    d = _CPU
+    g, T = d["g"], d["T"]
+    for s in segs:
+        b, h = divmod(s, d["Hkv"])
+        q = d["q"][b:b + 1, h * g:(h + 1) * g]
+        qbar, _ = O.query_prep(q, 1, d["tf"])
+        sc = O.score_tiles(qbar.reshape(-1, D), d["kb"][s:s + 1])
+        idx = O.topk_tiles(sc, d["k"])
+        O.decode_attention(q, d["wk"][b:b + 1, h:h + 1], d["wv"][b:b + 1, h:h + 1], d["kb"][s:s + 1],
+                           d["vb"][s:s + 1], d["ks"][s:s + 1], d["vs"][s:s + 1], idx, d["tf"])
+    return len(segs)
+
+
+def _cpu_encode(x):
+    from oracle import kvr_oracle as O
+    O.encode(x, _CPU["T"], _CPU["tf"])
+    return 1
+
+
+def _timed(fn, reps=5):
+    """1 warmup + the median of reps runs (seconds)."""
+    fn()
+    ts = []
+    for _ in range(reps):
         t0 = time.perf_counter()
-        while True:
-            qbar, _ = O.query_prep(q, Hkv, wl.transform)
-            sc = O.score_tiles(qbar.reshape(-1, D), kb)
-            idx = O.topk_tiles(sc, wl.k)
-            O.decode_attention(q, wk, wv, kb, vb, ks, vs, idx, wl.transform)
-            reps += 1
-            dt = time.perf_counter() - t0
-            if dt >= min_seconds:
-                break
-    match = bool(np.array_equal(idx, wl.idx.cpu().numpy()))
-    return {"value": round(reps * wl.B / dt, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle, 1 thread: {reps} whole-batch decode steps (B={wl.B}; query prep, "
-                      f"scores of {wl.n_tiles} tiles x {Hkv} KV heads, top-{wl.k}, float64 attention over "
-                      f"{wl.W} window tokens + the selected tiles) in {dt:.1f} s",
-            "topk_matches_gpu": match}
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Host threads for the all-core leg: the box's CPU share (16 per GPU) or fewer."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_decode(wl, threads):
+    """Median seconds of one whole-batch decode step of the numpy oracle over all B*Hkv
+    segments, serially (threads = 1) or split over a fork pool of `threads` workers."""
+    import multiprocessing as mp
+    from threadpoolctl import threadpool_limits
+    _CPU.clear()
+    _CPU.update(dict(q=wl.q.float().cpu().numpy(), wk=wl.win_k.float().cpu().numpy(),
+                     wv=wl.win_v.float().cpu().numpy(), kb=wl.kbits.cpu().numpy().view(np.uint64),
+                     vb=wl.vbits.cpu().numpy().view(np.uint64), ks=wl.kscale.cpu().numpy(),
+                     vs=wl.vscale.cpu().numpy(), g=wl.Hq // wl.Hkv, Hkv=wl.Hkv, T=wl.T, k=wl.k,
+                     tf=wl.transform))
+    n_seg = wl.B * wl.Hkv
+    with threadpool_limits(limits=1):
+        if threads == 1:
+            return _timed(lambda: _cpu_segments(range(n_seg)))
+        chunks = [list(range(i, n_seg, threads)) for i in range(min(threads, n_seg))]
+        with mp.get_context("fork").Pool(len(chunks)) as pool:
+            return _timed(lambda: pool.map(_cpu_segments, chunks))
+
+
+def cpu_encode_layer(threads, n_heads=8, N=16384, T=64, tf=H.HADAMARD):
+    """Median seconds to encode one configs[1] layer (K and V of n_heads x N tokens, the
+    numpy oracle: Hadamard, scale, sigma-delta, packing), serially or over a pool by head."""
+    import multiprocessing as mp
+    from threadpoolctl import threadpool_limits
+    g = np.random.default_rng(0)
+    xs = [(g.standard_normal((1, N, D)) * np.exp(g.standard_normal(D))).astype(np.float32)
+          for _ in range(2 * n_heads)]
+    _CPU.clear()
+    _CPU.update(T=T, tf=tf)
+    with threadpool_limits(limits=1):
+        if threads == 1:
+            return _timed(lambda: [_cpu_encode(x) for x in xs])
+        with mp.get_context("fork").Pool(min(threads, len(xs))) as pool:
+            return _timed(lambda: pool.map(_cpu_encode, xs))
+
+
+def cpu_configs0_workload():
+    """configs[0] on the host (fp32, built with the oracle codec): B=1, GQA 32/8, 4096 tokens,
+    window 512, 56 tiles of 64, top-8."""
+    from oracle import kvr_oracle as O
+
+    class W0:
+        pass
+    w = W0()
+    B, Hq, Hkv, N, Wn, T = 1, 32, 8, 4096, 512, 64
+    g = np.random.default_rng(0)
+    K = (g.standard_normal((B, Hkv, N, D)) * np.exp(g.standard_normal((1, Hkv, 1, D)))).astype(np.float32)
+    V = (g.standard_normal((B, Hkv, N, D)) * np.exp(g.standard_normal((1, Hkv, 1, D)))).astype(np.float32)
+    n_ret = N - Wn
+    kb, ks = O.encode(K[:, :, :n_ret].reshape(B * Hkv, n_ret, D), T, O.HADAMARD)
+    vb, vs = O.encode(V[:, :, :n_ret].reshape(B * Hkv, n_ret, D), T, O.HADAMARD)
+    w.q = torch.from_numpy(g.standard_normal((B, Hq, D)).astype(np.float32))
+    w.win_k, w.win_v = torch.from_numpy(K[:, :, n_ret:]), torch.from_numpy(V[:, :, n_ret:])
+    w.kbits, w.vbits = torch.from_numpy(kb.view(np.int64)), torch.from_numpy(vb.view(np.int64))
+    w.kscale, w.vscale = torch.from_numpy(ks), torch.from_numpy(vs)
+    w.B, w.Hq, w.Hkv, w.T, w.k, w.transform = B, Hq, Hkv, T, 8, O.HADAMARD
+    return w
+
+
+def cpu_baseline(wl, wl4, threads):
+    """The CPU restatement (numpy oracle, kind "port") on the host cores: the headline value is
+    configs[2]'s whole-batch decode step on `threads` threads (tokens/s); also reported at 1
+    thread, and configs[0], configs[4] decode and configs[1] encode (one layer, x 32) at both."""
+    model = _cpu_model()
+    res = {}
+    for th in (1, threads):
+        t2 = cpu_decode(wl, th)
+        res[f"cfg2_decode_tokens_per_s_{th}t"] = round(wl.B / t2, 3)
+        res[f"cfg2_step_s_{th}t"] = round(t2, 4)
+        if wl4 is not None:
+            t4 = cpu_decode(wl4, th)
+            res[f"cfg4_decode_tokens_per_s_{th}t"] = round(wl4.B / t4, 3)
+            res[f"cfg4_step_s_{th}t"] = round(t4, 4)
+        t0 = cpu_decode(cpu_configs0_workload(), th)
+        res[f"cfg0_decode_tokens_per_s_{th}t"] = round(1 / t0, 3)
+        heads = 2 if th == 1 else 8  # one thread: a quarter layer, scaled x 4
+        te = cpu_encode_layer(th, n_heads=heads) * (8 / heads)
+        nbytes = 2 * 8 * 16384 * D * 2 + 2 * 8 * 16384 * D // 8 + 2 * 8 * 256 * 2
+        res[f"cfg1_encode_s_32_layers_{th}t"] = round(32 * te, 3)
+        res[f"cfg1_encode_gbps_{th}t"] = round(nbytes / te / 1e9, 4)
+    return {"value": res[f"cfg2_decode_tokens_per_s_{threads}t"], "unit": "tokens/s", "cores": threads,
+            "kind": "port", "cpu": model, "host_cpus": os.cpu_count(),
+            "sample": f"numpy oracle (query prep, scores of all {wl.n_tiles} tiles x {wl.Hkv} KV heads, top-{wl.k}, "
+                      f"float64 attention over {wl.W} window tokens + the selected tiles) for configs[2]'s whole "
+                      f"batch of {wl.B}, over a fork pool of {threads} processes by segment; 1 warmup + median of "
+                      "5 runs.  breakdown: the same at 1 thread, configs[0] and configs[4] decode, configs[1] "
+                      "encode of one layer (K+V, 8 heads x 16384 tokens; at 1 thread 2 heads x 4) x 32",
+            "breakdown": res}
 
 
 def copy_calibration(nbytes=1 << 30, steps=20):
@@ -338,10 +483,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-encode", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
-    ap.add_argument("--no-rotate", action="store_true", help="skip the rotating-layers (HBM-resident) leg")
     ap.add_argument("--no-cfg4", action="store_true", help="skip the configs[4] (DCT, T=128) decode leg")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the configs[3] end-to-end decode leg")
+    ap.add_argument("--layers", type=int, default=4,
+                    help="layers of stores the headline step rotates through (their total exceeds the MALL)")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--e2e", action="store_true", help="also run the configs[3] end-to-end decode leg")
     ap.add_argument("--e2e-prompt", type=int, default=65536)
     ap.add_argument("--e2e-new", type=int, default=128)
     ap.add_argument("--e2e-layers", type=int, default=32)
@@ -361,59 +507,71 @@ def main():
         return
 
     log("building configs[2] workload (B=16, N=32768, W=1024, T=64, k=32) ...")
-    wl = DecodeWorkload()
-    log(f"  n_tiles={wl.n_tiles} W={wl.W}; warmup {args.warmup}, timing {args.steps} steps")
-    ms = time_events(wl.step, args.steps, args.warmup)
+    wl = DecodeWorkload(keep_keys=True)
     total, comp = wl.algorithmic_bytes()
+    log(f"  n_tiles={wl.n_tiles} W={wl.W}; warmup {args.warmup}, timing {args.steps} steps")
+    # headline: each step reads its layer's stores from HBM (the layers rotate; their total
+    # exceeds the 256 MB last-level cache), as in a multi-layer decode
+    wl.make_layers(args.layers)
+    ms = time_events(wl.step_rotating, args.steps, args.warmup)
     step_gbps = total / ms / 1e6
-    log(f"  decode step {ms * 1e3:.1f} us  ({step_gbps:.0f} GB/s algorithmic)")
+    log(f"  decode step, {args.layers} rotating layers (HBM-resident): {ms * 1e3:.2f} us ({step_gbps:.0f} GB/s algorithmic)")
+    del wl.layers
+    torch.cuda.empty_cache()
+    # the same layer re-read every step (its working set stays in the MALL)
+    mall_ms = time_events(wl.step, args.steps, args.warmup)
+    log(f"  decode step, one layer re-read (MALL-resident): {mall_ms * 1e3:.2f} us")
     # the same step scoring from the K bits instead of the per-tile channel counts
     kc, wl.kcount = wl.kcount, None
     bits_ms = time_events(wl.step, args.steps, args.warmup)
     bits_total, _ = wl.algorithmic_bytes()
     wl.kcount = kc
-    log(f"  decode step scoring from the K bits: {bits_ms * 1e3:.1f} us ({bits_total / bits_ms / 1e6:.0f} GB/s algorithmic)")
-
-    # the same step with each step's layer read from HBM (4 layers of stores > the MALL)
-    cold_ms = None
-    if not args.no_rotate:
-        wl.make_layers(4)
-        cold_ms = time_events(wl.step_rotating, args.steps, args.warmup)
-        del wl.layers
-        log(f"  decode step, 4 rotating layers (HBM-resident): {cold_ms * 1e3:.1f} us "
-            f"({total / cold_ms / 1e6:.0f} GB/s algorithmic)")
+    log(f"  decode step scoring from the K bits (MALL-resident): {bits_ms * 1e3:.2f} us")
 
     # DCT-II, T=128, B=4, GQA 28/4, context 131072, window 2048, top-64 tiles
-    cfg4 = {}
+    cfg4, wl4 = {}, None
     if not args.no_cfg4:
         log("building configs[4] workload (B=4, Hq=28, Hkv=4, N=131072, W=2048, T=128, k=64, DCT) ...")
         wl4 = DecodeWorkload(B=4, Hq=28, Hkv=4, N=131072, W=2048, T=128, k=64, transform=H.DCT, seed=4)
-        ms4 = time_events(wl4.step, args.steps, args.warmup)
         tot4, comp4 = wl4.algorithmic_bytes()
+        wl4.make_layers(6)
+        ms4 = time_events(wl4.step_rotating, args.steps, args.warmup)
+        del wl4.layers
+        torch.cuda.empty_cache()
+        ms4_mall = time_events(wl4.step, args.steps, args.warmup)
         cfg4 = {"cfg4_us_per_step": round(ms4 * 1e3, 2), "cfg4_tokens_per_s": round(wl4.B / (ms4 / 1e3), 1),
                 "cfg4_algorithmic_bytes": tot4, "cfg4_gbps": round(tot4 / ms4 / 1e6, 1),
-                "cfg4_roofline_frac": round(tot4 / ms4 / 1e6 / HBM_PEAK_GBPS, 4)}
-        log(f"  configs[4] step {ms4 * 1e3:.1f} us ({tot4 / ms4 / 1e6:.0f} GB/s algorithmic, "
-            f"{cfg4['cfg4_roofline_frac'] * 100:.1f} % of 8 TB/s)")
-        del wl4
-        torch.cuda.empty_cache()
+                "cfg4_roofline_frac": round(tot4 / ms4 / 1e6 / HBM_PEAK_GBPS, 4),
+                "cfg4_mall_resident_us_per_step": round(ms4_mall * 1e3, 2)}
+        log(f"  configs[4] step {ms4 * 1e3:.2f} us HBM-resident (6 rotating layers), {ms4_mall * 1e3:.2f} us "
+            f"MALL-resident ({tot4 / ms4 / 1e6:.0f} GB/s algorithmic, {cfg4['cfg4_roofline_frac'] * 100:.1f} % of 8 TB/s)")
 
     breakdown = {} if args.no_breakdown else kernel_breakdown(wl, 50)
     if breakdown:
         log("  breakdown (us): " + ", ".join(f"{k}={v * 1e3:.1f}" for k, v in breakdown.items()))
     recall = wl.planted_recall()
+    recall_exact = wl.planted_recall_exact()
+    log(f"  planted-tile recall {recall:.3f} (1-bit tiles); {recall_exact:.3f} with exact fp32 tile means")
     enc = {} if args.no_encode else encode_results(10)
     if enc:
         log(f"  encode configs[1]: {enc['encode_ms']:.3f} ms, {enc['encode_gbps']} GB/s; "
             f"configs[4] layer (DCT, T=128): {enc['cfg4_encode_ms']:.3f} ms, {enc['cfg4_encode_gbps']} GB/s")
+    cpu = None
+    if not args.no_cpu:
+        th = cpu_threads()
+        log(f"  cpu baseline (numpy oracle, 1 and {th} threads) ...")
+        cpu = cpu_baseline(wl, wl4, th)
+        cpu["topk_matches_gpu"] = None
+        log(f"  cpu baseline: {cpu['value']} tokens/s on {th} threads ({cpu['cpu']}); "
+            f"{cpu['breakdown']['cfg2_decode_tokens_per_s_1t']} on 1")
+    del wl4
+    torch.cuda.empty_cache()
     e2e = {}
-    if args.e2e:
+    if not args.no_e2e:
         log(f"configs[3] end-to-end: {args.e2e_layers} layers, prompt {args.e2e_prompt}, {args.e2e_new} new tokens ...")
         e2e = e2e_benchmark(args.e2e_prompt, args.e2e_new, args.e2e_layers)
-        log(f"  e2e decode: {e2e['e2e_decode_tokens_per_s']} tokens/s ({e2e['e2e_decode_ms_per_token']} ms/token)")
-    cpu = None if args.no_cpu else cpu_baseline(wl)
-    if cpu:
-        log(f"  cpu baseline: {cpu['value']} tokens/s ({cpu['sample']})")
+        log(f"  e2e decode: {e2e['e2e_decode_tokens_per_s']} tokens/s ({e2e['e2e_decode_ms_per_token']} ms/token, "
+            f"{e2e['e2e_graph_replays']} graph replays)")
 
     rec = {
         "metric": METRIC,
@@ -428,11 +586,12 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded K/V/q, RoPE base 500000, 16 planted keys per sequence)",
-        "config": {"workload": "configs[2] decode microbench: 1 layer, B=16, ctx 32768, GQA 32/8, d=128, "
-                               "bf16 window 1024, 1-bit Hadamard tiles of 64, top-32 tiles",
+        "config": {"workload": "configs[2] decode microbench: 1 layer per step, B=16, ctx 32768, GQA 32/8, d=128, "
+                               "bf16 window 1024, 1-bit Hadamard tiles of 64, top-32 tiles; the layer's stores "
+                               f"read from HBM (steps rotate over {args.layers} layers)",
                    "batch": wl.B, "context": wl.N, "window": wl.W, "tile": wl.T, "top_k_tiles": wl.k,
                    "n_tiles": wl.n_tiles, "transform": "hadamard"},
-        "roofline": {"bound": "hbm", "kernel": "kvr::step_kernel (the whole decode step, one launch)",
+        "roofline": {"bound": "hbm", "kernel": "kvr::step_kernel<64,bf16,1> (the whole decode step, one launch)",
                      "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": read_traffic("decode_step_decode32k.md"),
@@ -440,15 +599,17 @@ def main():
                      "compressed_gbps": round(comp / ms / 1e6, 1)},
         "cpu_baseline": cpu,
         "extra": {"planted_tile_recall": round(recall, 4),
+                  "planted_tile_recall_exact_tile_means": round(recall_exact, 4),
                   "tokens_per_s_32_layers": round(wl.B / (ms / 1e3) / 32, 1),
+                  "mall_resident_us_per_step": round(mall_ms * 1e3, 2),
+                  "mall_resident_tokens_per_s": round(wl.B / (mall_ms / 1e3), 1),
+                  "mall_resident_gbps": round(total / mall_ms / 1e6, 1),
                   "window_mfma_tflops": round(wl.window_flops() / ms / 1e9, 2),
                   "window_mfma_util_vs_bf16_dense": round(wl.window_flops() / ms / 1e9 / BF16_DENSE_TFLOPS, 5),
                   "scan_bits_us_per_step": round(bits_ms * 1e3, 2),
                   "scan_bits_algorithmic_bytes": bits_total,
                   "scan_bits_gbps": round(bits_total / bits_ms / 1e6, 1),
-                  **cfg4, **e2e,
-                  "rotating_4_layers_us_per_step": round(cold_ms * 1e3, 2) if cold_ms else None,
-                  "rotating_4_layers_gbps": round(total / cold_ms / 1e6, 1) if cold_ms else None, **enc,
+                  **cfg4, **e2e, **enc,
                   **{k: round(v, 5) for k, v in breakdown.items()}},
     }
     print(json.dumps(rec))

@@ -77,6 +77,9 @@ int check_window(const void* wk, const void* wv, int wdt, int64_t win_len, int64
   if (win_start < 0 || (win_cap > 0 ? win_start >= win_cap : win_start != 0))
     return fail(KVR_ERR_INVALID, "win_start=%lld outside the ring (capacity %lld; 0 without a ring)",
                 (long long)win_start, (long long)win_cap);
+  if (win_cap % 32 || win_start % 32)
+    return fail(KVR_ERR_INVALID, "a ring's capacity and start must be multiples of 32 (%lld, %lld)",
+                (long long)win_cap, (long long)win_start);
   if (win_len == 0 && win_cap == 0) return KVR_OK;
   if (!valid_dtype(wdt)) return fail(KVR_ERR_INVALID, "window dtype %d unknown", wdt);
   if (!wk || !wv) return fail(KVR_ERR_INVALID, "window pointers are NULL");

@@ -24,8 +24,9 @@
 // attend_kernel -> merge_kernel.
 //
 // Partial records: per segment s and part p, g*(2+128) floats: m2[g] (running max,
-// log2 units), l[g], o[g][128].  Window parts hold o in the original domain,
-// retrieved parts in the rotated domain (rotated back once per head in the merge).
+// log2 units), l[g], o[g][128]; the retrieved parts first, then the window parts.
+// Window parts hold o in the original domain, retrieved parts in the rotated domain
+// (rotated back once per head in the merge).
 // The window may be a ring (win_cap > 0): logical token i of the win_len valid ones is
 // in slot (win_start + i) mod win_cap.  With a live state (decode step only) the
 // window length, ring start and tile count are read per segment from device memory,
@@ -204,21 +205,17 @@ __device__ __forceinline__ uint64_t cand_load(const uint64_t* p) {
 // word and the high half the tag's high 32 bits, so a reader that finds the expected
 // tag halves in both words has this call's entry of that list, whenever it reads -- no
 // completion wait and counter on the writer's side, no poll before the read.  The tag
-// is a bijective 64-bit mix (the splitmix64 finaliser) of the injective packing
-// epoch | segment << 32 | list << 52 (segment < 2^20, list < 2^12), so entries of any
-// other (epoch, segment, list) -- an earlier call, another workspace layout -- never
-// validate; zeroed memory never does either (the tag is never 0).  The epoch is per
-// segment (fused step: the segment's epoch word + 1, advanced by the segment's merging
-// item) or CAND_EPOCH_CHAIN when the lists are written by an earlier launch.
+// is the injective packing epoch << 32 | segment | list << 20 | 1 << 31 (segment <
+// 2^20, list < 2^11), so an entry of any other (epoch, segment, list) -- an earlier
+// call, another workspace layout -- never validates, and zeroed memory never does
+// either (bit 31 is set).  The high half, which a waiting reader polls, is the epoch:
+// the previous call's list in the same slot fails the poll.  The epoch is per segment
+// (fused step: the segment's epoch word + 1, advanced by the segment's merging item) or
+// CAND_EPOCH_CHAIN when the lists are written by an earlier launch.
 constexpr uint32_t CAND_EPOCH_CHAIN = 0xffffffffu;
 constexpr uint32_t WAIT_FAIL_EPOCH = 0x5bd1e995u;  // xor-ed into the expected epoch by the wait_fail hook
 __device__ __forceinline__ uint64_t cand_tag(uint32_t epoch, int64_t seg, int list) {
-  uint64_t z = (uint64_t)epoch | ((uint64_t)((uint32_t)seg & 0xfffffu) << 32) |
-               ((uint64_t)((uint32_t)list & 0xfffu) << 52);
-  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  z ^= z >> 31;
-  return z ? z : 1ull;  // never 0: zeroed memory is never a valid entry
+  return ((uint64_t)epoch << 32) | ((uint32_t)seg & 0xfffffu) | (((uint32_t)list & 0x7ffu) << 20) | (1u << 31);
 }
 __device__ __forceinline__ void cand_put(uint64_t* list, int e, uint64_t v, uint64_t tag) {
   cand_store(list + 2 * e, (tag << 32) | (v & 0xffffffffull));
@@ -968,15 +965,26 @@ __device__ void write_record_stats(const CombineSmem& cs, float* R, int g, int t
 
 // ------------------------------------------------------------------ window role (MFMA)
 
-// Slot of logical window token tok (0 <= tok < win_len): the ring start is added and
-// wrapped at the ring capacity (win_start < win_cap and win_len <= win_cap).
-__device__ __forceinline__ int64_t win_slot(const DecodeArgs& a, int64_t tok) {
-  const int64_t s = tok + a.win_start;
-  return (a.win_cap > 0 && s >= a.win_cap) ? s - a.win_cap : s;
+// Window rows of a chunk of up to 32 logical tokens from c0 (c0 a multiple of 16).  Without
+// a ring (RING false) row r is token c0 + r, clamped to the last token past win_len (the
+// row is masked; the buffer may end there).  With a ring, row r is slot p0 + r, p0 = c0 +
+// the ring start wrapped at the capacity: starts and capacities are multiples of 32 (the
+// host checks), so a chunk never straddles the wrap and its rows past win_len stay inside
+// the ring (masked).  p0 is uniform across the wave.
+__device__ __forceinline__ int64_t ring_chunk_slot(const DecodeArgs& a, int64_t c0) {
+  const int64_t s = c0 + a.win_start;
+  return s >= a.win_cap ? s - a.win_cap : s;
+}
+template <bool RING>
+__device__ __forceinline__ int64_t window_row(const DecodeArgs& a, int64_t c0, int64_t p0, int r) {
+  if constexpr (RING) return p0 + r;
+  const int64_t t = c0 + r;
+  return t < a.win_len ? t : a.win_len - 1;
 }
 
-// Partial record of a segment: window part p at index p, retrieved part r at
-// n_wparts_cap + r, n_wparts_cap + n_rparts records per segment.
+// Partial record of a segment: retrieved part r at index r, window part p at n_rparts + p,
+// n_rparts + n_wparts_cap records per segment (live window parts fewer than the capacity
+// leave the last slots unused, so the live records are always indices [0, n_parts)).
 __device__ __forceinline__ float* rec_ptr(const DecodeArgs& a, int64_t seg, int index) {
   return a.rec + (seg * (a.n_wparts_cap + a.n_rparts) + index) * (int64_t)(a.g * (2 + D));
 }
@@ -1007,7 +1015,7 @@ typedef void __attribute__((address_space(3))) * lds_ptr_t;
 // K comes straight into registers in A-operand order; V rows go from HBM to the wave's
 // LDS rows by direct 16-byte LDS loads (lane l of load i: token 4i + l/16, dims
 // 8 (l%16) ..), both issued before the query is read.
-template <int WDT, int QS, int PS>
+template <int WDT, int QS, int PS, bool RING>
 __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
   constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
   const int tid = threadIdx.x;
@@ -1028,21 +1036,17 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 
   u32x4 ka[2][4];
   auto issue_chunk = [&](int64_t c0) {
+    const int64_t p0 = RING ? ring_chunk_slot(a, c0) : c0;
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
-      int64_t tok = c0 + 16 * tb + n;
-      tok = tok < win_len ? tok : win_len - 1;  // clamped rows are masked below
-      const uint16_t* kr = kbase + win_slot(a, tok) * st + 8 * kg;
+      const uint16_t* kr = kbase + window_row<RING>(a, c0, p0, 16 * tb + n) * st + 8 * kg;  // rows past the end: masked
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) ka[tb][ks] = *(const u32x4*)(kr + 32 * ks);
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int64_t tok = c0 + 4 * i + kg;
-      tok = tok < win_len ? tok : win_len - 1;
-      __builtin_amdgcn_global_load_lds((const void*)(vbase + win_slot(a, tok) * st + 8 * n),
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(vbase + window_row<RING>(a, c0, p0, 4 * i + kg) * st + 8 * n),
                                        (lds_ptr_t)(vs + i * 4 * D), 16, 0, 0);
-    }
   };
   int64_t c0 = t_begin + (int64_t)wv_id * WIN_CHUNK;
   if (c0 < t_end) issue_chunk(c0);
@@ -1164,7 +1168,7 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
   l_run += xor16_f(l_run);
   l_run += xor32_f(l_run);
   // oacc[i][r] of lane (n, kg) is dim 32 kg + 8 r + i
-  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, rec_ptr(a, seg, part),
+  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, rec_ptr(a, seg, a.n_rparts + part),
                  [](int i, int r, int kgv) { return 32 * kgv + 8 * r + i; });
 }
 
@@ -1180,7 +1184,7 @@ __device__ void window_role(const DecodeArgs& a, int64_t seg, int part, WindowSm
 //   as the A operands of the eight dim blocks j (D row m <-> dim 8 m + j).
 // The record layout matches the 16-bit window role: oacc[j][r] of lane (n, kg) is dim
 // 32 kg + 8 r + j.
-template <int QT>
+template <int QT, bool RING>
 __device__ void window_role_f32(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1220,11 +1224,10 @@ __device__ void window_role_f32(const DecodeArgs& a, int64_t seg, int part, Wind
   float l_run = 0.f;
 
   for (int64_t c0 = t_begin + 16 * (int64_t)wv_id; c0 < t_end; c0 += 64) {
+    const int64_t p0 = RING ? ring_chunk_slot(a, c0) : c0;
     float kv[32];
     {
-      int64_t tok = c0 + n;
-      tok = tok < win_len ? tok : win_len - 1;  // clamped rows are masked below
-      const float4* kr = (const float4*)(kbase + win_slot(a, tok) * st + 32 * kg);
+      const float4* kr = (const float4*)(kbase + window_row<RING>(a, c0, p0, n) * st + 32 * kg);  // past the end: masked
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float4 f = kr[i];
@@ -1237,9 +1240,7 @@ __device__ void window_role_f32(const DecodeArgs& a, int64_t seg, int part, Wind
     float vv[4][8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      int64_t tok = c0 + 4 * kg + r;
-      tok = tok < win_len ? tok : win_len - 1;
-      const float4* vr = (const float4*)(vbase + win_slot(a, tok) * st + 8 * n);
+      const float4* vr = (const float4*)(vbase + window_row<RING>(a, c0, p0, 4 * kg + r) * st + 8 * n);
       const float4 f0 = vr[0], f1 = vr[1];
       vv[r][0] = f0.x; vv[r][1] = f0.y; vv[r][2] = f0.z; vv[r][3] = f0.w;
       vv[r][4] = f1.x; vv[r][5] = f1.y; vv[r][6] = f1.z; vv[r][7] = f1.w;
@@ -1279,15 +1280,20 @@ __device__ void window_role_f32(const DecodeArgs& a, int64_t seg, int part, Wind
 
   l_run += xor16_f(l_run);
   l_run += xor32_f(l_run);
-  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, rec_ptr(a, seg, part),
+  combine_record(oacc, m_run, l_run, sm.ow, sm.cs, g, rec_ptr(a, seg, a.n_rparts + part),
                  [](int j, int r, int kgv) { return 32 * kgv + 8 * r + j; });
 }
 
-// The window role for the window's dtype.
-template <int WDT, int QS>
+// The window role for the window's dtype and layout (a plain run of slots or a ring).
+template <int WDT, int QS, bool RING>
 __device__ __forceinline__ void window_item(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
-  if constexpr (WDT == KVR_FP32) window_role_f32<(QS == 1) ? KVR_FP32 : Q_RUNTIME>(a, seg, part, sm);
-  else window_role<WDT, QS, 3>(a, seg, part, sm);
+  if constexpr (WDT == KVR_FP32) window_role_f32<(QS == 1) ? KVR_FP32 : Q_RUNTIME, RING>(a, seg, part, sm);
+  else window_role<WDT, QS, 3, RING>(a, seg, part, sm);
+}
+template <int WDT, int QS>
+__device__ __forceinline__ void window_item_any(const DecodeArgs& a, int64_t seg, int part, WindowSmem& sm) {
+  if (a.win_cap > 0) window_item<WDT, QS, true>(a, seg, part, sm);
+  else window_item<WDT, QS, false>(a, seg, part, sm);
 }
 
 // Query heads h0, h0 + step, ... (up to QH_MAX of them, the slots a wave rotates) of a
@@ -1610,6 +1616,7 @@ struct RetMfmaSmem {
     float ow[4 * OW_WAVE];    // per-wave partial o' (after the tile loop)
   } u;
   CombineSmem cs;
+  int fail[4];                // per wave: its selection's bounded wait gave up
 };
 
 __device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
@@ -1753,7 +1760,9 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     }
     sm.u.pm1[x] = u32x4{w[0], w[1], w[2], w[3]};
   }
-  const bool poison = __syncthreads_or(failed ? 1 : 0) != 0;  // any wave's wait gave up
+  sm.fail[wv_id] = failed ? 1 : 0;  // each wave its own flag: no clearing before the barrier
+  __syncthreads();
+  const bool poison = (sm.fail[0] | sm.fail[1] | sm.fail[2] | sm.fail[3]) != 0;  // any wave's wait gave up
   const int32_t* sel = sm.u.sel;
   if (par) {
     uint64_t acc = sm.u.p.part[0][lane];
@@ -1883,18 +1892,16 @@ __device__ __forceinline__ void merge_parts(const DecodeArgs& a, const float* R0
                                             float& M, float& L, float& w0, float& w1, float& r0, float& r1) {
   const int g = a.g;
   const int n_parts = a.n_wparts + a.n_rparts;
-  const int gap = a.n_wparts_cap - a.n_wparts;  // live window parts < the record slots reserved for them
-  auto pidx = [&](int p) { return p < a.n_wparts ? p : p + gap; };
   for (int p0 = 0; p0 < n_parts; p0 += MAXP) {
     const bool mine = lane < MAXP && p0 + lane < n_parts;  // this lane's part of the batch
-    const float* Rl = R0 + pidx(mine ? p0 + lane : p0) * rs;
+    const float* Rl = R0 + (mine ? p0 + lane : p0) * rs;
     const float pm = rec_load(Rl + i);
     const float pl = rec_load(Rl + g + i);
     float2 po[MAXP];
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
       const int pc = (p0 + p < n_parts) ? p0 + p : n_parts - 1;
-      po[p] = rec_load2(R0 + pidx(pc) * rs + 2 * g + i * D + 2 * lane);
+      po[p] = rec_load2(R0 + pc * rs + 2 * g + i * D + 2 * lane);
     }
     const float Mn = fmaxf(M, wave_max(mine ? pm : -__builtin_inff()));
     const float mu = (Mn == -__builtin_inff()) ? 0.f : Mn;
@@ -1909,12 +1916,12 @@ __device__ __forceinline__ void merge_parts(const DecodeArgs& a, const float* R0
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
       const float fp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), p));  // 0 past the end
-      if (p0 + p < a.n_wparts) {
-        w0 = fmaf(po[p].x, fp, w0);
-        w1 = fmaf(po[p].y, fp, w1);
-      } else {
+      if (p0 + p < a.n_rparts) {
         r0 = fmaf(po[p].x, fp, r0);
         r1 = fmaf(po[p].y, fp, r1);
+      } else {
+        w0 = fmaf(po[p].x, fp, w0);
+        w1 = fmaf(po[p].y, fp, w1);
       }
     }
   }
@@ -2123,12 +2130,12 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs
     p = (int)(blockIdx.x - seg * parts);
   }
   if (p < a.n_rparts) {
-    float* R = rec_ptr(a, seg, a.n_wparts_cap + p);
+    float* R = rec_ptr(a, seg, p);
     constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
     if constexpr (RM == 0) retrieved_role_mfma<T, QT>(a, seg, p, sm.retm, R);
     else retrieved_role<T, G4, QT>(a, seg, p, sm.ret, R);
   } else {
-    window_item<WDT, QS>(a, seg, p - a.n_rparts, sm.win);
+    window_item_any<WDT, QS>(a, seg, p - a.n_rparts, sm.win);
   }
 }
 
@@ -2177,11 +2184,53 @@ struct StepSmem {
   int last;
 };
 
-template <int T, int WDT, int QS>
-__global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a_in) {
-  __shared__ StepSmem sm;
+// The work of one step_kernel block, given its item (chunk >= 0: score item; wp >= 0:
+// window item; else retrieved item rp).
+template <int T, int WDT, int QS, bool RING>
+__device__ __forceinline__ void step_item(const DecodeArgs& a, StepSmem& sm, int64_t it, int64_t seg, int chunk,
+                                          int wp, int rp) {
   constexpr int QT = (QS == 1) ? WDT : Q_RUNTIME;  // QS == 1: the query has the window's dtype
   const int tid = threadIdx.x;
+  int32_t* epoch = a.ctr + CTR_HDR;                       // [seg * CTR_STRIDE] the segment's epoch
+  int32_t* rdone = epoch + STEP_MAX_SEG * CTR_STRIDE;    // [seg * CTR_STRIDE] records done
+  if (chunk >= 0) {
+    if (chunk >= a.n_chunks) return;  // past the live tiles
+    const uint32_t ep = (uint32_t)ctr_load(epoch + seg * CTR_STRIDE) + 1u;  // used when the list is stored
+    score_item<T, QT>(a, seg, chunk, (int)(it & 3), sm.u.sc, ep);
+    return;
+  }
+  if (wp >= a.n_wparts) return;  // past the live window
+  const int parts = a.n_wparts + a.n_rparts;
+  if (wp >= 0) {
+    window_item<WDT, QS, RING>(a, seg, wp, sm.u.win);
+  } else {
+    retrieved_role_mfma<T, QT>(a, seg, rp, sm.u.retm, rec_ptr(a, seg, rp), epoch + seg * CTR_STRIDE);
+  }
+  wait_vm();  // record stored
+  __syncthreads();
+  if (tid == 0) sm.last = ctr_add(rdone + seg * CTR_STRIDE, 1) == parts - 1;
+  __syncthreads();
+  if (sm.last) {
+    if (tid == 0) {  // every item of the segment is past its counters
+      ctr_add(epoch + seg * CTR_STRIDE, 1);
+      ctr_store(rdone + seg * CTR_STRIDE, 0);
+    }
+    const int w = tid >> 6;
+    if (a.transform == KVR_DCT && a.n_rparts > 0) merge_segment_rot(a, seg, sm.u.mg);
+    else
+      for (int hh = w; hh < a.g; hh += 4) merge_head(a, seg, hh, tid & 63, sm.u.xs[w]);
+  }
+}
+
+// LIVE: the window is a ring and its length, ring start and tile count of the block's
+// segment come from the live state (the grid covers the capacities); else the window is a
+// plain run of slots and everything comes from the arguments.  DCT: the transform is the
+// DCT; else Hadamard or none -- fixed at compile time, so a launch carries only its own
+// rotation code (the kernel's instruction footprint is what its concurrently running roles
+// share in the instruction cache).
+template <int T, int WDT, int QS, bool DCT, bool LIVE>
+__global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a_in) {
+  __shared__ StepSmem sm;
   const int64_t S = a_in.n_seg;
   // block -> work item, over the capacities (= the live counts without a live state)
   const int64_t n_score = S * a_in.n_chunks_cap, n_win = S * a_in.n_wparts_cap, n_ret = S * a_in.n_rparts;
@@ -2208,10 +2257,10 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a
       else rp = (int)(jj - seg * per);
     }
   }
-  // The segment's live window length, ring start and tile count (clamped to the
-  // capacities the grid and the buffers were sized for), and what follows from them.
   DecodeArgs a = a_in;
-  if (a.live) {
+  a.transform = DCT ? KVR_DCT : (a_in.transform == KVR_NONE ? KVR_NONE : KVR_HADAMARD);
+  if constexpr (LIVE) {
+    // the segment's live counts, clamped to the capacities the grid and buffers were sized for
     const int32_t* ls = a.live + seg * 4;
     const int64_t wl = ls[0], ws = ls[1], nt = ls[2];
     a.win_len = wl < 0 ? 0 : (wl > a_in.win_len ? a_in.win_len : wl);
@@ -2221,36 +2270,7 @@ __global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void step_kernel(DecodeArgs a
     a.n_wparts = (int)((a.win_len + a.win_span - 1) / a.win_span);
     if (a.n_wparts == 0 && a.n_rparts == 0) a.n_wparts = 1;  // an empty window item still writes the output (zeros)
   }
-  int32_t* epoch = a.ctr + CTR_HDR;                       // [seg * CTR_STRIDE] the segment's epoch
-  int32_t* rdone = epoch + STEP_MAX_SEG * CTR_STRIDE;    // [seg * CTR_STRIDE] records done
-  if (chunk >= 0) {
-    if (chunk >= a.n_chunks) return;  // past the live tiles
-    const uint32_t ep = (uint32_t)ctr_load(epoch + seg * CTR_STRIDE) + 1u;  // used when the list is stored
-    score_item<T, QT>(a, seg, chunk, (int)(it & 3), sm.u.sc, ep);
-    return;
-  }
-  if (wp >= a.n_wparts) return;  // past the live window
-  const int parts = a.n_wparts + a.n_rparts;
-  if (wp >= 0) {
-    window_item<WDT, QS>(a, seg, wp, sm.u.win);
-  } else {
-    retrieved_role_mfma<T, QT>(a, seg, rp, sm.u.retm, rec_ptr(a, seg, a.n_wparts_cap + rp),
-                               epoch + seg * CTR_STRIDE);
-  }
-  wait_vm();  // record stored
-  __syncthreads();
-  if (tid == 0) sm.last = ctr_add(rdone + seg * CTR_STRIDE, 1) == parts - 1;
-  __syncthreads();
-  if (sm.last) {
-    if (tid == 0) {  // every item of the segment is past its counters
-      ctr_add(epoch + seg * CTR_STRIDE, 1);
-      ctr_store(rdone + seg * CTR_STRIDE, 0);
-    }
-    const int w = tid >> 6;
-    if (a.transform == KVR_DCT && a.n_rparts > 0) merge_segment_rot(a, seg, sm.u.mg);
-    else
-      for (int hh = w; hh < a.g; hh += 4) merge_head(a, seg, hh, tid & 63, sm.u.xs[w]);
-  }
+  step_item<T, WDT, QS, LIVE>(a, sm, it, seg, chunk, wp, rp);
 }
 
 // Bytes of the counter region that starts every decode workspace.
@@ -2536,16 +2556,22 @@ hipError_t launch_decode(const DecodeLaunch& L, hipStream_t s) {
     hipLaunchKernelGGL(zero_out_kernel, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, a, n);
     return hipGetLastError();
   }
-  const bool fused = L.do_select && step_is_fused(BH, L.k, L.ctr != nullptr) && a.cand;
+  // the one-launch step takes a ring window exactly when it takes a live state (a ring
+  // without one runs the launch chain, whose window role handles both layouts)
+  const bool fused = L.do_select && step_is_fused(BH, L.k, L.ctr != nullptr) && a.cand &&
+                     ((L.live != nullptr) == (L.win_cap > 0));
   if (L.live && !fused) return hipErrorInvalidValue;  // the host rejects this before launching
   if (fused) {
     a.scores = nullptr;  // the one-launch step keeps no score array
     const int64_t tickets = BH * (a.n_chunks_cap + a.n_wparts_cap + a.n_rparts);  // blocks = work items
     const bool same = (qt == wdt);
+#define KVR_ST_L(TV, WV, QSV, DV)                                                                     \
+  if (a.live) hipLaunchKernelGGL((step_kernel<TV, WV, QSV, DV, true>), dim3((unsigned)tickets), dim3(NT), 0, s, a); \
+  else hipLaunchKernelGGL((step_kernel<TV, WV, QSV, DV, false>), dim3((unsigned)tickets), dim3(NT), 0, s, a);
 #define KVR_ST(TV, WV, QSV) \
-  hipLaunchKernelGGL((step_kernel<TV, WV, QSV>), dim3((unsigned)tickets), dim3(NT), 0, s, a);
+  if (a.transform == KVR_DCT) { KVR_ST_L(TV, WV, QSV, true) } else { KVR_ST_L(TV, WV, QSV, false) }
 #define KVR_ST_Q(TV, WV) \
-  if (same) KVR_ST(TV, WV, 1) else KVR_ST(TV, WV, 3)
+  if (same) { KVR_ST(TV, WV, 1) } else { KVR_ST(TV, WV, 3) }
     if (T == 64 && wdt == KVR_FP16) { KVR_ST_Q(64, KVR_FP16) }
     else if (T == 64 && wdt == KVR_FP32) { KVR_ST_Q(64, KVR_FP32) }
     else if (T == 64) { KVR_ST_Q(64, KVR_BF16) }
@@ -2554,6 +2580,7 @@ hipError_t launch_decode(const DecodeLaunch& L, hipStream_t s) {
     else { KVR_ST_Q(128, KVR_BF16) }
 #undef KVR_ST_Q
 #undef KVR_ST
+#undef KVR_ST_L
     return hipGetLastError();
   }
   if (a.do_select) {

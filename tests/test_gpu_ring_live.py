@@ -120,9 +120,11 @@ def test_ring_window_equals_unrolled(H, rng, wdt):
 @pytest.mark.parametrize("T,tf", [(64, O.HADAMARD), (128, O.DCT)])
 def test_live_state_equals_host_arguments(H, rng, T, tf):
     """Reading the window length, ring start and tile count from the device state runs the
-    same work as passing them from the host: identical tiles selected and identical outputs,
+    same work as passing them from the host (with the ring's tokens laid out in order, the
+    one-launch step's plain-window form): identical tiles selected and identical outputs,
     for live counts below the capacities the launch is sized for (and fewer live tiles
-    than k: every stored tile is taken)."""
+    than k: every stored tile is taken).  A ring without a live state (the launch chain)
+    selects the same tiles and meets the oracle's bar."""
     say(f"[live] T={T} tf={tf}")
     B, Hq, Hkv, k = 2, 28 if tf == O.DCT else 32, 4 if tf == O.DCT else 8, 5
     W = 2 * T
@@ -138,20 +140,30 @@ def test_live_state_equals_host_arguments(H, rng, T, tf):
         out_l = H.decode_step(q, ring_k, ring_v, cap - 1, kb, vb, ks, vs, tile_cap, T, tf, k, out_dtype=torch.float32,
                               idx_out=idx_l, workspace=ws, kcounts=kc, win_cap=cap, live_state=state)
         ke = min(k, n_tiles)
+        order = (torch.arange(n, device=DEV) + start) % cap
+        flat_k, flat_v = ring_k[:, :, order].contiguous(), ring_v[:, :, order].contiguous()
         idx_h = torch.empty((B * Hkv, ke), dtype=torch.int32, device=DEV)
-        out_h = H.decode_step(q, ring_k, ring_v, n, kb, vb, ks, vs, n_tiles, T, tf, ke, out_dtype=torch.float32,
-                              idx_out=idx_h, kcounts=kc, win_start=start, win_cap=cap)
+        out_h = H.decode_step(q, flat_k, flat_v, n, kb, vb, ks, vs, n_tiles, T, tf, ke, out_dtype=torch.float32,
+                              idx_out=idx_h, kcounts=kc)
+        idx_c = torch.empty((B * Hkv, ke), dtype=torch.int32, device=DEV)
+        out_c = H.decode_step(q, ring_k, ring_v, n, kb, vb, ks, vs, n_tiles, T, tf, ke, out_dtype=torch.float32,
+                              idx_out=idx_c, kcounts=kc, win_start=start, win_cap=cap)
         torch.cuda.synchronize()
         il = idx_l.cpu().numpy()
         assert np.array_equal(il[:, :ke], idx_h.cpu().numpy()), (n, start, n_tiles)
+        assert np.array_equal(il[:, :ke], idx_c.cpu().numpy()), (n, start, n_tiles)
         assert (il[:, ke:] == -1).all()
-        assert torch.equal(out_l, out_h), (n, start, n_tiles)
+        per = max(8 * 64 // T, 4)  # selected tiles per retrieved item
+        if -(-k // per) == -(-ke // per):  # the same partial records: the same sums, bit for bit
+            assert torch.equal(out_l, out_h), (n, start, n_tiles)
+        # (with more retrieved items than tiles, the live launch merges an extra empty record:
+        # the same value up to the order of the merge's sums, held to the oracle's bar below)
         assert H.workspace_status(ws) == 0
-        order = (torch.arange(n, device=DEV) + start) % cap
         ref = O.decode_attention(q.float().cpu().numpy(), ring_k[:, :, order].float().cpu().numpy(),
                                  ring_v[:, :, order].float().cpu().numpy(), u64(kb), u64(vb), ks.cpu().numpy(),
                                  vs.cpu().numpy(), il[:, :ke], tf)
         check_out(out_l, ref, f"live n={n} start={start} n_tiles={n_tiles}")
+        check_out(out_c, ref, f"ring, launch chain n={n} start={start} n_tiles={n_tiles}")
 
 
 # ----------------------------------------------------------------------------- ring append
