@@ -268,15 +268,14 @@ __device__ __forceinline__ void qbar_load(const DecodeArgs& a, int64_t seg, int 
   }
 }
 
+// The GQA-mean query's channels (2 lane, 2 lane + 1) from the raw loads of qbar_load.
 template <int QT>
-__device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, uint32_t* r1, float* qs, float* xs,
-                                            int lane, const DctRegs& dt) {
+__device__ __forceinline__ void qbar_mean(const DecodeArgs& a, uint32_t* r0, uint32_t* r1, float& m0, float& m1) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     pin(r0[i]);
     if (QT == Q_RUNTIME || QT == KVR_FP32) pin(r1[i]);  // r1 is a constant 0 for 16-bit dtypes
   }
-  float m0, m1;
   q_pair_cvt<QT>(a, r0[0], r1[0], m0, m1);
 #pragma unroll
   for (int i = 1; i < 16; ++i) {
@@ -289,6 +288,47 @@ __device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, u
   }
   m0 = __fdiv_rn(m0, (float)a.g);
   m1 = __fdiv_rn(m1, (float)a.g);
+}
+
+// Outputs k in [32 w, 32 w + 32) of y = C x (DCT-II) for a vector x held by the calling
+// wave w as channels (2 lane, 2 lane + 1), into y_out[k]: each of the block's four waves
+// calls it with its own scratch xs (the table staged at xs + D), and y_out holds all 128
+// outputs after a block barrier.  With C[k][127 - n] = (-1)^k C[k][n], output k sums 64
+// terms C[k][n] t[n] (t = x[n] + x[127 - n] for even k, x[n] - x[127 - n] for odd k),
+// split over a lane pair (n < 32 and n >= 32) and added once: a quarter of dct_pair's
+// LDS reads per lane.  Tolerance path (fmaf).
+__device__ __forceinline__ void dct_quarter(float v0, float v1, int lane, int w, float* xs, float* y_out) {
+  const float* cs = xs + D;
+  xs[2 * lane] = v0;
+  xs[2 * lane + 1] = v1;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const float xa = xs[lane], xb = xs[127 - lane];
+  __builtin_amdgcn_wave_barrier();
+  ((float2*)xs)[lane] = make_float2(xa + xb, xa - xb);  // (s[n], d[n]) at n = lane
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const int k = 32 * w + (lane >> 1), h = lane & 1;
+  // table index of C[k][n]: (2n+1) k mod 512, stepping by 2k from n = 32 h; row 0 stays at 512
+  int r = (k == 0) ? 512 : ((64 * h + 1) * k) & 511;
+  const int dr = (k == 0) ? 0 : (2 * k) & 511, msk = (k == 0) ? 1023 : 511;
+  const bool odd = k & 1;
+  float acc = 0.f;
+#pragma unroll 8
+  for (int i = 0; i < 32; ++i) {
+    const float2 sd = ((const float2*)xs)[32 * h + i];
+    acc = fmaf(cs[r], odd ? sd.y : sd.x, acc);
+    r = (r + dr) & msk;
+  }
+  acc = acc + xor_lane_f<1>(acc);
+  if (h == 0) y_out[k] = acc;
+}
+
+template <int QT>
+__device__ __forceinline__ void qbar_finish(const DecodeArgs& a, uint32_t* r0, uint32_t* r1, float* qs, float* xs,
+                                            int lane, const DctRegs& dt) {
+  float m0, m1;
+  qbar_mean<QT>(a, r0, r1, m0, m1);
   if (a.transform == KVR_DCT) dct_table_store(dt, xs, lane);
   rotate_pair(m0, m1, lane, a.transform, xs);
   qs[2 * lane] = m0;
@@ -2054,9 +2094,9 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int 
   const int32_t hi = a.excl_hi ? a.excl_hi[seg] : 0;
   // Every wave builds the query mean itself (straight-line loads from L2, issued first:
   // loads complete in issue order, so the prologue runs while the words stream in) and
-  // scores its tiles as soon as its own words are in, with no block barrier before the
-  // sort.  The sort runs on wave helper_wave (the item number mod 4), so the items
-  // resident on a CU spread it over the four SIMDs.
+  // scores its tiles as soon as its own words are in (Hadamard: with no block barrier
+  // before the sort).  The sort runs on wave helper_wave (the item number mod 4), so the
+  // items resident on a CU spread it over the four SIMDs.
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const bool helper = wv == helper_wave;
@@ -2064,18 +2104,31 @@ __device__ void score_item(const DecodeArgs& a, int64_t seg, int64_t chunk, int 
   qbar_load<QT>(a, seg, lane, qv0, qv1);
   DctRegs dt{};
   if (a.transform == KVR_DCT) dt = dct_table_load(lane);  // before the words: no wait on them
+  // The rotated mean query: a Hadamard rotation is a few lane exchanges, done by every wave
+  // for itself; a DCT is shared out over the four waves (dct_quarter) and met at a barrier.
+  auto query = [&]() -> const float* {
+    if (a.transform == KVR_DCT) {
+      float m0, m1;
+      qbar_mean<QT>(a, qv0, qv1, m0, m1);
+      dct_table_store(dt, sm.xs[wv], lane);
+      dct_quarter(m0, m1, lane, wv, sm.xs[wv], sm.qs[0]);
+      __syncthreads();
+      return sm.qs[0];
+    }
+    qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane, dt);
+    wave_lds_sync();
+    return sm.qs[wv];
+  };
   if (a.kcount) {  // the count summary: 8 bytes per lane and tile instead of 8 words
     ScoreCounts<T> sc;
     counts_load<T>(a.kcount, seg, a.tile_stride, t0, t1, sc);
-    qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane, dt);
-    wave_lds_sync();
-    score_compute_counts<T>(sm.qs[wv], sc, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
+    const float* qs = query();
+    score_compute_counts<T>(qs, sc, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
   } else {
     ScoreWords<T> sw;
     score_load<T>(a.kbits, seg, a.tile_stride, t0, t1, sw);
-    qbar_finish<QT>(a, qv0, qv1, sm.qs[wv], sm.xs[wv], lane, dt);
-    wave_lds_sync();
-    score_compute<T, 0>(sm.qs[wv], sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
+    const float* qs = query();
+    score_compute<T, 0>(qs, sw, seg, a.n_tiles, t0, t1, lo, hi, a.scores, a.cand ? sm.lc : nullptr);
   }
   if (a.cand) {
     __syncthreads();
