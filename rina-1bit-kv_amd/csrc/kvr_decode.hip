@@ -57,6 +57,13 @@ constexpr int NT = 256;           // threads per block (4 waves) for every decod
 #ifndef KVR_WIN_MIN_ITEMS
 #define KVR_WIN_MIN_ITEMS 256
 #endif
+#ifndef KVR_MERGE_PB
+#define KVR_MERGE_PB 3  // parts per wave in the parts-split merge (g in 5..8, n_parts <= 4 KVR_MERGE_PB): one
+                        // load batch of 8 heads x KVR_MERGE_PB parts stays clear of spills
+#endif
+#ifndef KVR_WIN_MAX_PARTS
+#define KVR_WIN_MAX_PARTS 4  // window items per segment (at most, spans allowing) when tiles are retrieved
+#endif
 #ifndef KVR_CAND_MAX
 #define KVR_CAND_MAX 64  // k up to which score items write sorted candidate lists (0: never)
 #endif
@@ -1420,7 +1427,7 @@ struct RetSmem {
 template <int W>
 struct TileWords {
   uint64_t k0[W], k1[W], v0[W], v1[W];
-  float sk, sv;
+  uint32_t sk, sv;  // fp16 bits of the tile's scales (converted where used)
 };
 
 template <int T>
@@ -1438,8 +1445,8 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int64_t seg, int6
     tw.v0[w] = vp[lane * W + w];
     tw.v1[w] = vp[(lane + 64) * W + w];
   }
-  tw.sk = f16_to_f32(a.kscale[slot]);
-  tw.sv = f16_to_f32(a.vscale[slot]);
+  tw.sk = a.kscale[slot];
+  tw.sv = a.vscale[slot];
 }
 
 // All selected tiles of one segment in one block: wave w takes tiles w, w+4, ...
@@ -1525,6 +1532,7 @@ __device__ __forceinline__ void retrieved_role(const DecodeArgs& a, int64_t seg,
   for (int j = j0; j < k; j += 4 * RS) {
     if (j + 4 * RS < k)
       load_tile<T>(a, seg, sm.sel[j + 4 * RS], lane, nxt);
+    const float sk = f16_to_f32(cur.sk), sv = f16_to_f32(cur.sv);
 #pragma unroll 1
     for (int w = 0; w < W; ++w) {
       uint32_t a_lo = (uint32_t)cur.k0[w], a_hi = (uint32_t)(cur.k0[w] >> 32);
@@ -1551,7 +1559,7 @@ __device__ __forceinline__ void retrieved_role(const DecodeArgs& a, int64_t seg,
       float alpha[G4], psum[G4];
 #pragma unroll
       for (int hh = 0; hh < G4; ++hh) {
-        const float lg = cur.sk * (2.f * dot[hh] - sm.qsum[hh]) * SCALE_LOG2;
+        const float lg = sk * (2.f * dot[hh] - sm.qsum[hh]) * SCALE_LOG2;
         const float m_new = fmaxf(m_run[hh], wave_max(lg));
         alpha[hh] = fast_exp2(m_run[hh] - m_new);
         m_run[hh] = m_new;
@@ -1597,8 +1605,8 @@ __device__ __forceinline__ void retrieved_role(const DecodeArgs& a, int64_t seg,
       }
 #pragma unroll
       for (int hh = 0; hh < G4; ++hh) {
-        o0[hh] = o0[hh] * alpha[hh] + cur.sv * (2.f * x0[hh] - psum[hh]);
-        o1[hh] = o1[hh] * alpha[hh] + cur.sv * (2.f * x1[hh] - psum[hh]);
+        o0[hh] = o0[hh] * alpha[hh] + sv * (2.f * x0[hh] - psum[hh]);
+        o1[hh] = o1[hh] * alpha[hh] + sv * (2.f * x1[hh] - psum[hh]);
       }
       wave_lds_sync();  // ps / lu are rewritten by the next sub-tile
     }
@@ -1678,7 +1686,8 @@ __device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
 struct MfmaUnit {
   uint64_t kw[2];  // K channel words of channels lane and lane + 64 (bit-transpose rows)
   uint64_t vw[8];  // V channel words of channels 16 cb + n
-  float sk, sv;
+  uint32_t sk, sv;  // fp16 bits of the tile's scales, converted where used (a conversion
+                    // next to the loads would wait for them: no fetch ahead)
 };
 
 template <int T>
@@ -1694,8 +1703,8 @@ __device__ __forceinline__ void fetch_mfma_unit(const DecodeArgs& a, int64_t seg
   t.kw[1] = kp[(lane + 64) * W];
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) t.vw[cb] = vp[(16 * cb + n) * W];
-  t.sk = f16_to_f32(a.kscale[slot]) * SCALE_LOG2;
-  t.sv = f16_to_f32(a.vscale[slot]);
+  t.sk = a.kscale[slot];
+  t.sv = a.vscale[slot];
 }
 
 // epoch_word (fused step): the segment's epoch word; the selection reads the lists of
@@ -1825,7 +1834,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     MfmaUnit nxt;  // the wave's next unit, fetched while this one is processed
     if (u + 1 < n_units)
       fetch_mfma_unit<T>(a, seg, sel[j0 + ((u + 1) / W) * jstep], (u + 1) % W, lane, nxt);
-    const float sk = cur.sk, sv = cur.sv;
+    const float sk = f16_to_f32((uint16_t)cur.sk) * SCALE_LOG2, sv = f16_to_f32((uint16_t)cur.sv);
     {
       uint32_t row[4] = {(uint32_t)cur.kw[0], (uint32_t)(cur.kw[0] >> 32), (uint32_t)cur.kw[1],
                          (uint32_t)(cur.kw[1] >> 32)};
@@ -2001,63 +2010,328 @@ __device__ void merge_head(const DecodeArgs& a, int64_t seg, int i, int lane, fl
   }
 }
 
-// Whole-segment merge for DCT segments with retrieved parts, on the block's four waves.
-// Phase A: every head's sums (one wave per head) into LDS as [channel][head] columns.
-// Phase B: the retrieved sums of all heads are rotated back at once on MFMA, wave w
-// taking output channels [32 w, 32 w + 32): out[n][h] = (W[n][h] + sum_k C[k][n] R[k][h])
-// / L[h], as 16x16x4 fp32 products (C^T rows from the matrix in constant memory, loaded
-// before phase A so they arrive meanwhile).  Head columns past g are not stored.
+// ---- whole-segment merge on the block's four waves
+//
+// Phase A gathers every head's window sums W and retrieved sums R (each part scaled to
+// the head's max over all parts) into LDS slots [kind][slot][head][channel]:
+//   parts-split (4 < g <= 8, n_parts <= 4 KVR_MERGE_PB): wave w takes parts w, w + 4, ...
+//     for every head at once -- one load batch -- and every wave holds every
+//     part's max and sum (lane p: part p), so all four scale to the same per-head max;
+//     the four waves' sums go to four slots, added in slot order where used;
+//   per head (otherwise): wave w takes heads w, w + 4, ... (merge_sums), one slot.
+// Phase B rotates R back and stores (W + R_unrotated) / L:
+//   DCT on MFMA: x = C^T y with the rows of C even or odd about n -> 127 - n
+//     (C[k][127 - n] = (-1)^k C[k][n]), so wave w forms for its 16 output channels
+//     n = 16 w + m the even-row sum E and the odd-row sum O (K = 64 each) and writes
+//     x[n] = E + O and x[127 - n] = E - O: 12 fp16 16x16x32 products per wave with both
+//     operands split into two fp16 parts (hi * hi + hi * lo + lo * hi, ~22-bit products,
+//     fp32 accumulation); R enters already divided by L (fp16 range), C enters times 8
+//     (fewer fp16 subnormals among its low parts), the table in constant memory holds
+//     C's parts in operand order;
+//   Hadamard / none: wave w takes heads w, w + 4, ... (in-register Hadamard).
+constexpr int MG_PITCH = D + 4;  // floats per head row (padded: conflict-free 16-byte columns)
+constexpr int MG_FLOATS = 2 * 4 * 8 * MG_PITCH;  // 2 kinds x 4 slots x 8 heads (or 1 slot x 16 heads)
 struct MergeSmem {
-  float rt[D][17];  // retrieved sums [channel][head] (row padded: conflict-free columns)
-  float wt[D][17];  // window sums
-  float inv[16];    // 1 / L per head
+  float buf[MG_FLOATS];
+  float inv[16];  // 1 / L per head
 };
+static_assert(2 * 1 * 16 * MG_PITCH <= MG_FLOATS, "one slot of 16 heads");
+__device__ __forceinline__ float* mg_row(MergeSmem& ms, int kind, int slot, int nslots, int g, int head) {
+  return ms.buf + ((kind * nslots + slot) * g + head) * MG_PITCH;
+}
 
-__device__ void merge_segment_rot(const DecodeArgs& a, int64_t seg, MergeSmem& ms) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int g = a.g;
-  const int hc = lane & 15;  // head column (B and D operands), row of A
-  const int kq = lane >> 4;  // k within a step (A and B), row group of D
-  // A[m][kk] = C^T[32 w + 16 mb + m][4 ks + kk] = C[4 ks + kk][32 w + 16 mb + m]
-  float av[2][32];
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int ks = 0; ks < 32; ++ks) av[mb][ks] = g_dct[(4 * ks + kq) * D + 32 * w + 16 * mb + hc];
-
-  for (int hh = w; hh < g; hh += 4) {
-    float L, w0, w1, r0, r1;
-    merge_sums(a, seg, hh, lane, L, w0, w1, r0, r1);
-    ms.rt[2 * lane][hh] = r0;
-    ms.rt[2 * lane + 1][hh] = r1;
-    ms.wt[2 * lane][hh] = w0;
-    ms.wt[2 * lane + 1][hh] = w1;
-    if (lane == 0) ms.inv[hh] = (L > 0.f) ? 1.f / L : 0.f;
+// fp16 parts of C (times 8) in MFMA A-operand order: [w][eo][ks][part][lane] x 8 halves,
+// lane (m, kq) element e = C[2 (32 ks + 8 kq + e) + eo][16 w + m] * 8, rounded to nearest
+// even at compile time (hi = fp16(x), lo = fp16(x - hi)).
+constexpr uint32_t f16_bits_rne(double x) {
+  uint32_t sign = 0;
+  if (x < 0) {
+    sign = 0x8000u;
+    x = -x;
   }
-  __syncthreads();
-
-  float bv[32];  // B[kk][h] = R[4 ks + kk][h]
-#pragma unroll
-  for (int ks = 0; ks < 32; ++ks) bv[ks] = ms.rt[4 * ks + kq][hc];
-  const float inv = hc < g ? ms.inv[hc] : 0.f;
-  const int64_t bq = (seg / a.Hkv) * a.Hq + (seg % a.Hkv) * g + hc;  // b * Hq + head
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    const int n0 = 32 * w + 16 * mb + 4 * kq;  // D rows n0 .. n0 + 3 of head column hc
-    f32x4 acc = f32x4{ms.wt[n0][hc], ms.wt[n0 + 1][hc], ms.wt[n0 + 2][hc], ms.wt[n0 + 3][hc]};
-#pragma unroll
-    for (int ks = 0; ks < 32; ++ks) acc = mfma16_f32(av[mb][ks], bv[ks], acc);
-    if (hc < g) {
-      const int64_t o = bq * D + n0;
-      if (a.out_dtype == KVR_FP32) {
-        *(float4*)((float*)a.out + o) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
-      } else {
-        *(uint2*)((uint16_t*)a.out + o) = make_uint2(pack2(f32_to_bf16_rne(acc[0] * inv), f32_to_bf16_rne(acc[1] * inv)),
-                                                     pack2(f32_to_bf16_rne(acc[2] * inv), f32_to_bf16_rne(acc[3] * inv)));
-      }
+  if (x == 0.0) return sign;
+  int e = 0;
+  double p = 1.0;  // 2^e, x in [p, 2p) (or the subnormal range at e = -14)
+  while (x >= 2.0 * p) {
+    p *= 2.0;
+    ++e;
+  }
+  while (x < p && e > -14) {
+    p *= 0.5;
+    --e;
+  }
+  const double m = x / (p / 1024.0);  // exact: a power-of-two quantum
+  uint32_t mi = (uint32_t)m;
+  const double fr = m - (double)mi;
+  if (fr > 0.5 || (fr == 0.5 && (mi & 1u))) ++mi;
+  if (mi >= 1024u) {
+    if (mi == 2048u) {
+      mi = 1024u;
+      ++e;
     }
+    return sign | ((uint32_t)(e + 15) << 10) | (mi - 1024u);
+  }
+  return sign | mi;
+}
+constexpr double f16_value(uint32_t b) {
+  const int ex = (int)((b >> 10) & 31u);
+  double v = (ex == 0) ? (double)(b & 1023u) : (double)(1024u + (b & 1023u));
+  for (int sh = (ex == 0) ? -24 : ex - 25; sh != 0; sh += (sh < 0) ? 1 : -1) v = (sh < 0) ? v * 0.5 : v * 2.0;
+  return (b & 0x8000u) ? -v : v;
+}
+struct DctF16Table {
+  uint32_t v[4 * 2 * 2 * 2 * 64 * 4];
+};
+constexpr DctF16Table make_dct_f16_table() {
+  DctF16Table t{};
+  double c[512] = {};
+  for (int r = 0; r < 512; ++r) c[r] = cos_pi_r256(r);
+  for (int w = 0; w < 4; ++w)
+    for (int eo = 0; eo < 2; ++eo)
+      for (int ks = 0; ks < 2; ++ks)
+        for (int lane = 0; lane < 64; ++lane)
+          for (int e = 0; e < 8; ++e) {
+            const int n = 16 * w + (lane & 15);
+            const int k = 2 * (32 * ks + 8 * (lane >> 4) + e) + eo;
+            const double sc = (k == 0) ? 0.088388347648318440550 : 0.125;
+            const double x = (double)(float)(sc * c[((2 * n + 1) * k) % 512]) * 8.0;  // the fp32 C entry
+            const uint32_t hi = f16_bits_rne(x);
+            const uint32_t lo = f16_bits_rne(x - f16_value(hi));
+            const int at = ((((w * 2 + eo) * 2 + ks) * 2) * 64 + lane) * 4 + (e >> 1);
+            t.v[at] |= hi << (16 * (e & 1));
+            t.v[at + 64 * 4] |= lo << (16 * (e & 1));
+          }
+  return t;
+}
+constexpr DctF16Table kDctF16 = make_dct_f16_table();
+static __constant__ DctF16Table g_dct16 = kDctF16;
+
+// A operands of wave w: [eo * 4 + ks * 2 + part]
+__device__ __forceinline__ void dct16_load(int w, int lane, u32x4 (&A)[8]) {
+  const u32x4* t = (const u32x4*)g_dct16.v + w * 8 * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) A[i] = t[i * 64];
+}
+
+// Block barrier over LDS only: LDS accesses complete and stay on their side of it; global
+// loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ void store_out4(const DecodeArgs& a, int64_t o, float y0, float y1, float y2, float y3) {
+  if (a.out_dtype == KVR_FP32) {
+    *(float4*)((float*)a.out + o) = make_float4(y0, y1, y2, y3);
+  } else {
+    *(uint2*)((uint16_t*)a.out + o) = make_uint2(pack2(f32_to_bf16_rne(y0), f32_to_bf16_rne(y1)),
+                                                 pack2(f32_to_bf16_rne(y2), f32_to_bf16_rne(y3)));
+  }
+}
+
+// Phase A, parts-split (see above): G >= g heads, n_parts <= 4 PB (one load batch).
+template <int G, int PB>
+__device__ void merge_gather_split(const DecodeArgs& a, int64_t seg, MergeSmem& ms, int lane, int w) {
+  const int g = a.g;
+  const int P = a.n_wparts + a.n_rparts;
+  const int nr = a.n_rparts;
+  const int64_t rs = (int64_t)g * (2 + D);
+  const float* R0 = rec_ptr(a, seg, 0);
+  const bool mine = lane < P;  // lane p holds part p's max and sum
+  const float* Rl = R0 + (mine ? lane : P - 1) * rs;
+  // (every address below is a per-part base plus a constant head offset: loads of heads
+  // past g are skipped, not clamped -- a clamped head index would cost an address per load)
+  float pm[G], pq[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    pm[i] = -__builtin_inff();
+    pq[i] = 0.f;
+    if (i < g) {
+      pm[i] = rec_load(Rl + i);
+      pq[i] = rec_load(Rl + g + i);
+    }
+  }
+  const int npw = (P > w) ? (P - w + 3) / 4 : 0;  // parts of wave w
+  float2 o[G][PB];  // in flight while the weights are formed
+#pragma unroll
+  for (int j = 0; j < PB; ++j) {
+    int p = w + 4 * j;
+    p = p < P ? p : P - 1;
+    const float* Rp = R0 + p * rs + 2 * g + 2 * lane;
+#pragma unroll
+    for (int i = 0; i < G; ++i) o[i][j] = (i < g) ? rec_load2(Rp + i * D) : make_float2(0.f, 0.f);
+  }
+  float f[G], L[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const float mx = wave_max(mine ? pm[i] : -__builtin_inff());
+    const float mu = (mx == -__builtin_inff()) ? 0.f : mx;
+    f[i] = mine ? fast_exp2(pm[i] - mu) : 0.f;
+    L[i] = wave_sum(mine ? pq[i] * f[i] : 0.f);
+  }
+  // per head: the wave's parts in order, then the sums to the wave's slot (one head's
+  // sums live at a time; the head's loads are dead after it)
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    if (i < g) {
+      float r0 = 0.f, r1 = 0.f, w0 = 0.f, w1 = 0.f;
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        const int p = w + 4 * j;
+        if (j < npw) {
+          const float fp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f[i]), p));
+          const float fr = p < nr ? fp : 0.f, fw = p < nr ? 0.f : fp;
+          r0 = fmaf(o[i][j].x, fr, r0);
+          r1 = fmaf(o[i][j].y, fr, r1);
+          w0 = fmaf(o[i][j].x, fw, w0);
+          w1 = fmaf(o[i][j].y, fw, w1);
+        }
+      }
+      ((float2*)mg_row(ms, 0, w, 4, g, i))[lane] = make_float2(w0, w1);
+      ((float2*)mg_row(ms, 1, w, 4, g, i))[lane] = make_float2(r0, r1);
+      if (w == 0 && lane == 0) ms.inv[i] = (L[i] > 0.f) ? 1.f / L[i] : 0.f;
+    }
+  }
+}
+
+// Phase B, DCT (see above).  nslots: slots of phase A; A: the wave's C operands.
+__device__ void merge_unrotate_dct(const DecodeArgs& a, int64_t seg, MergeSmem& ms, int nslots, const u32x4 (&A)[8],
+                                   int lane, int w) {
+  const int g = a.g;
+  const int hc = lane & 15;  // head column of B and D
+  const int kq = lane >> 4;  // k group of B, row group of D
+  const int hs = hc < g ? hc : g - 1;
+  const float inv = hc < g ? ms.inv[hc] : 0.f;
+  // B[kk][h] = R[2 (32 ks + kk) + eo][h] / L[h]: for ks, the lane's 16 channels 64 ks + 16 kq + i
+  u32x4 Bv[8];  // [eo * 4 + ks * 2 + part]
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float4 t = ((const float4*)(mg_row(ms, 1, 0, nslots, g, hs) + 64 * ks + 16 * kq))[q];
+      for (int sl = 1; sl < nslots; ++sl) {
+        const float4 u = ((const float4*)(mg_row(ms, 1, sl, nslots, g, hs) + 64 * ks + 16 * kq))[q];
+        t.x += u.x;
+        t.y += u.y;
+        t.z += u.z;
+        t.w += u.w;
+      }
+      v[4 * q] = t.x * inv;
+      v[4 * q + 1] = t.y * inv;
+      v[4 * q + 2] = t.z * inv;
+      v[4 * q + 3] = t.w * inv;
+    }
+#pragma unroll
+    for (int eo = 0; eo < 2; ++eo) {
+      uint32_t hi[8], lo[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t pp[2];
+        split16<KVR_FP16, 2>(v[2 * e + eo], pp);
+        hi[e] = pp[0];
+        lo[e] = pp[1];
+      }
+      Bv[eo * 4 + ks * 2] = u32x4{pack2(hi[0], hi[1]), pack2(hi[2], hi[3]), pack2(hi[4], hi[5]), pack2(hi[6], hi[7])};
+      Bv[eo * 4 + ks * 2 + 1] = u32x4{pack2(lo[0], lo[1]), pack2(lo[2], lo[3]), pack2(lo[4], lo[5]), pack2(lo[6], lo[7])};
+    }
+  }
+  f32x4 acc[2];
+#pragma unroll
+  for (int eo = 0; eo < 2; ++eo) {
+    acc[eo] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int b = eo * 4 + ks * 2;
+      acc[eo] = mfma16_f16(A[b], Bv[b], acc[eo]);
+      acc[eo] = mfma16_f16(A[b], Bv[b + 1], acc[eo]);
+      acc[eo] = mfma16_f16(A[b + 1], Bv[b], acc[eo]);
+    }
+  }
+  if (hc < g) {
+    const int n0 = 16 * w + 4 * kq;  // rows n0 .. n0 + 3, mirrors 127 - n0 .. 124 - n0
+    float4 wl = *(const float4*)(mg_row(ms, 0, 0, nslots, g, hc) + n0);
+    float4 wh = *(const float4*)(mg_row(ms, 0, 0, nslots, g, hc) + 124 - n0);
+    for (int sl = 1; sl < nslots; ++sl) {
+      const float4 ul = *(const float4*)(mg_row(ms, 0, sl, nslots, g, hc) + n0);
+      const float4 uh = *(const float4*)(mg_row(ms, 0, sl, nslots, g, hc) + 124 - n0);
+      wl.x += ul.x; wl.y += ul.y; wl.z += ul.z; wl.w += ul.w;
+      wh.x += uh.x; wh.y += uh.y; wh.z += uh.z; wh.w += uh.w;
+    }
+    const float el[4] = {wl.x, wl.y, wl.z, wl.w}, eh[4] = {wh.w, wh.z, wh.y, wh.x};  // eh[r]: channel 127 - n0 - r
+    float yl[4], yh[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float E = acc[0][r] * 0.125f, O = acc[1][r] * 0.125f;
+      yl[r] = fmaf(el[r], inv, E + O);
+      yh[r] = fmaf(eh[r], inv, E - O);
+    }
+    const int64_t bq = (seg / a.Hkv) * a.Hq + (seg % a.Hkv) * g + hc;  // b * Hq + head
+    store_out4(a, bq * D + n0, yl[0], yl[1], yl[2], yl[3]);
+    store_out4(a, bq * D + 124 - n0, yh[3], yh[2], yh[1], yh[0]);
+  }
+}
+
+// Phase B, Hadamard or none, after a parts-split phase A: wave w takes heads w, w + 4, ...
+__device__ void merge_finish_split(const DecodeArgs& a, int64_t seg, MergeSmem& ms, int lane, int w) {
+  const int g = a.g;
+  for (int hh = w; hh < g; hh += 4) {
+    float2 ws = ((const float2*)mg_row(ms, 0, 0, 4, g, hh))[lane];
+    float2 rv = ((const float2*)mg_row(ms, 1, 0, 4, g, hh))[lane];
+#pragma unroll
+    for (int sl = 1; sl < 4; ++sl) {
+      const float2 u = ((const float2*)mg_row(ms, 0, sl, 4, g, hh))[lane];
+      const float2 t = ((const float2*)mg_row(ms, 1, sl, 4, g, hh))[lane];
+      ws.x += u.x;
+      ws.y += u.y;
+      rv.x += t.x;
+      rv.y += t.y;
+    }
+    if (a.n_rparts > 0 && a.transform == KVR_HADAMARD) hadamard_pair(rv.x, rv.y, lane);
+    const float inv = ms.inv[hh];
+    const float y0 = (ws.x + rv.x) * inv, y1 = (ws.y + rv.y) * inv;
+    const int64_t o = ((seg / a.Hkv) * a.Hq + (seg % a.Hkv) * g + hh) * D + 2 * lane;
+    if (a.out_dtype == KVR_FP32) {
+      ((float2*)a.out)[o >> 1] = make_float2(y0, y1);
+    } else {
+      ((uint32_t*)a.out)[o >> 1] = pack2(f32_to_bf16_rne(y0), f32_to_bf16_rne(y1));
+    }
+  }
+}
+
+// The merge of one segment by the block of its last record (all four waves).
+__device__ void merge_segment(const DecodeArgs& a, int64_t seg, MergeSmem& ms, float (*xs)[DCT_SCRATCH], int tid) {
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = a.g;
+  const bool dct = a.transform == KVR_DCT && a.n_rparts > 0;
+  const bool split = g > 4 && g <= 8 && a.n_wparts + a.n_rparts <= 4 * KVR_MERGE_PB;
+  if (!dct && !split) {  // one head per wave (and round trip)
+    for (int hh = w; hh < g; hh += 4) merge_head(a, seg, hh, lane, xs[w]);
+    return;
+  }
+  int nslots = 4;
+  if (split) {
+    merge_gather_split<8, KVR_MERGE_PB>(a, seg, ms, lane, w);
+  } else {
+    nslots = 1;
+    for (int hh = w; hh < g; hh += 4) {
+      float L, w0, w1, r0, r1;
+      merge_sums(a, seg, hh, lane, L, w0, w1, r0, r1);
+      ((float2*)mg_row(ms, 0, 0, 1, g, hh))[lane] = make_float2(w0, w1);
+      ((float2*)mg_row(ms, 1, 0, 1, g, hh))[lane] = make_float2(r0, r1);
+      if (lane == 0) ms.inv[hh] = (L > 0.f) ? 1.f / L : 0.f;
+    }
+  }
+  if (dct) {
+    u32x4 A[8];
+    dct16_load(w, lane, A);  // in flight across the barrier
+    lds_barrier();
+    merge_unrotate_dct(a, seg, ms, nslots, A, lane, w);
+  } else {
+    lds_barrier();
+    merge_finish_split(a, seg, ms, lane, w);
   }
 }
 
@@ -2268,10 +2542,7 @@ __device__ __forceinline__ void step_item(const DecodeArgs& a, StepSmem& sm, int
       ctr_add(epoch + seg * CTR_STRIDE, 1);
       ctr_store(rdone + seg * CTR_STRIDE, 0);
     }
-    const int w = tid >> 6;
-    if (a.transform == KVR_DCT && a.n_rparts > 0) merge_segment_rot(a, seg, sm.u.mg);
-    else
-      for (int hh = w; hh < a.g; hh += 4) merge_head(a, seg, hh, tid & 63, sm.u.xs[w]);
+    merge_segment(a, seg, sm.u.mg, sm.u.xs, tid);
   }
 }
 
@@ -2451,14 +2722,21 @@ __global__ __launch_bounds__(64) void gather_tiles_kernel(const uint64_t* __rest
 
 // Window tokens per window item: one 32-token chunk per wave (128) unless the
 // segments x window are large enough to keep >= KVR_WIN_MIN_ITEMS window items with
-// longer spans (fewer partial records for the merge); at most 16 chunks per wave.
-int64_t window_span(int64_t BH, int64_t win_len) {
+// longer spans (fewer partial records for the merge); at most 16 chunks per wave.  With
+// retrieved tiles (k > 0) a segment's window takes at most KVR_WIN_MAX_PARTS items where
+// spans allow: the window items then finish well inside the retrieved items' latency
+// chain, and the merge loads fewer records.
+int64_t window_span(int64_t BH, int64_t win_len, int k) {
   int64_t s = (BH * win_len) / ((int64_t)WIN_UNIT * KVR_WIN_MIN_ITEMS);
+  if (k > 0) {
+    const int64_t sp = (win_len + (int64_t)WIN_UNIT * KVR_WIN_MAX_PARTS - 1) / ((int64_t)WIN_UNIT * KVR_WIN_MAX_PARTS);
+    s = s > sp ? s : sp;
+  }
   s = s < 1 ? 1 : (s > 16 ? 16 : s);
   return s * WIN_UNIT;
 }
-int n_window_parts(int64_t BH, int64_t win_len) {
-  const int64_t span = window_span(BH, win_len);
+int n_window_parts(int64_t BH, int64_t win_len, int k) {
+  const int64_t span = window_span(BH, win_len, k);
   return (win_len > 0) ? (int)((win_len + span - 1) / span) : 0;
 }
 constexpr int RET_TILES_PER_BLOCK = KVR_RET_TILES;  // selected tiles per retrieved item
@@ -2472,7 +2750,7 @@ int n_retrieved_parts(int k, int T) {
 // Partial records in the workspace: one per window item and per retrieved item.
 size_t records_bytes(int64_t B, int Hq, int Hkv, int64_t win_len, int k, int T) {
   const int g = Hq / Hkv;
-  const int64_t parts = n_window_parts(B * Hkv, win_len) + n_retrieved_parts(k, T);
+  const int64_t parts = n_window_parts(B * Hkv, win_len, k) + n_retrieved_parts(k, T);
   return (size_t)(B * Hkv * (parts > 0 ? parts : 1) * g * (2 + D)) * sizeof(float);
 }
 
@@ -2588,8 +2866,8 @@ hipError_t launch_decode(const DecodeLaunch& L, hipStream_t s) {
   a.idx = L.idx;
   a.rec = L.rec;
   a.n_chunks = (int)((L.n_tiles + score_tiles_per_item(T) - 1) / score_tiles_per_item(T));
-  a.n_wparts = n_window_parts(B * L.Hkv, L.win_len);
-  a.win_span = window_span(B * L.Hkv, L.win_len);
+  a.n_wparts = n_window_parts(B * L.Hkv, L.win_len, L.k);
+  a.win_span = window_span(B * L.Hkv, L.win_len, L.k);
   a.n_rparts = n_retrieved_parts(L.k, T);
   a.n_chunks_cap = a.n_chunks;
   a.n_wparts_cap = a.n_wparts;
