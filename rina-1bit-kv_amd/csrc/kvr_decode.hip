@@ -1387,6 +1387,17 @@ __device__ __forceinline__ uint32_t tstage(uint32_t x, int lane, uint32_t m) {
   return (lane & S) ? ((x & ~m) | ((p >> S) & m)) : ((x & m) | ((p & m) << S));
 }
 
+// The low four stages of transpose64 on one 32-bit word of the 64 channel words held
+// one per lane (bit t of lane c: token t of channel c): lane bits 0..3 are swapped with
+// bit-index bits 0..3, so lane (c5 c4 t3 t2 t1 t0) holds, at bit (t4 c3 c2 c1 c0), the
+// bit of channel (c5 c4 c3 c2 c1 c0) and token (t4 t3 t2 t1 t0) of the word.
+__device__ __forceinline__ void transpose_rows16(uint32_t& x, int lane) {
+  x = tstage<8>(x, lane, 0x00ff00ffu);
+  x = tstage<4>(x, lane, 0x0f0f0f0fu);
+  x = tstage<2>(x, lane, 0x33333333u);
+  x = tstage<1>(x, lane, 0x55555555u);
+}
+
 __device__ __forceinline__ void transpose64(uint32_t& lo, uint32_t& hi, int lane) {
   {
     // stage 32: lower lanes take the partner's lo as hi, upper lanes its hi as lo
@@ -1675,8 +1686,11 @@ __device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
 // Retrieved tiles of one segment on MFMA (fp16 inputs, fp32 accumulate).  Block rs of
 // the segment's RS blocks: wave w takes tiles rs*4 + w, then + 4*RS, ...
 //   S^T[16 tok x 16 heads] = Khat[16 tok x 32 ch] Q'^T[32 ch x 16 heads]: Khat = +-1
-//     from the token rows (64x64 bit transpose, then the byte of the row holding the
-//     lane's 8 channels, fetched from the row's lane), Q' split in 2 fp16 parts.
+//     from a partial bit transpose of the channel words (transpose_rows16: lane
+//     (m, kq) then holds tokens 16 tb + m of channels 16 kq + 8 s + e, s < 2, e < 8,
+//     tb < 4, so every A operand is a byte of the lane's own words -- no lane
+//     exchange), k-step ks taking channels 64 (ks / 2) + 16 kq + 8 (ks % 2) + e;
+//     Q' in that channel order, split in 2 fp16 parts.
 //   O'^T[16 ch x 16 heads] += Vhat^T[16 ch x 32 tok] (sv P)^T[32 tok x 16 heads]: the
 //     S^T accumulator slots are the PV k-slots (as in the window part); Vhat^T = +-1
 //     from two nibbles of the lane's channel word; sv*P split in 2 fp16 parts.
@@ -1718,7 +1732,6 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv_id = tid >> 6;
-  const int n = lane & 15;   // head column / token or channel row
   const int kg = lane >> 4;  // k-slot group
   const int g = a.g;
   const int kp = a.k;  // pitch of the idx rows
@@ -1783,12 +1796,13 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
           rotate_pair(x0, x1, lane, a.transform, sm.u.xs[wv_id]);
         }
         // Q'^T operand (B) of head column hh: lane (hh, kg) of k-step ks holds
-        // q'[hh][32 ks + 8 kg + e], e < 8, in 2 fp16 parts; this lane's channels 2 lane,
-        // 2 lane + 1 are k-step lane / 16, slot group (lane / 4) % 4, word lane % 4
+        // q'[hh][64 (ks / 2) + 16 kg + 8 (ks % 2) + e], e < 8, in 2 fp16 parts; this
+        // lane's channels 2 lane, 2 lane + 1 are k-step 2 (lane / 32) + (lane / 4) % 2,
+        // slot group (lane / 8) % 4, word lane % 4
         uint32_t p0[RP], p1[RP];
         split16<KVR_FP16, RP>(x0, p0);
         split16<KVR_FP16, RP>(x1, p1);
-        uint32_t* q32 = (uint32_t*)&sm.u.qb[lane >> 4][0][hh + 16 * ((lane >> 2) & 3)];
+        uint32_t* q32 = (uint32_t*)&sm.u.qb[2 * (lane >> 5) + ((lane >> 2) & 1)][0][hh + 16 * ((lane >> 3) & 3)];
 #pragma unroll
         for (int sp = 0; sp < RP; ++sp) q32[sp * 64 * 4 + (lane & 3)] = pack2(p0[sp], p1[sp]);
       }
@@ -1838,8 +1852,8 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
     {
       uint32_t row[4] = {(uint32_t)cur.kw[0], (uint32_t)(cur.kw[0] >> 32), (uint32_t)cur.kw[1],
                          (uint32_t)(cur.kw[1] >> 32)};
-      transpose64(row[0], row[1], lane);  // lane t: token t, channels 0..63
-      transpose64(row[2], row[3], lane);  // channels 64..127
+#pragma unroll
+      for (int i = 0; i < 4; ++i) transpose_rows16(row[i], lane);  // row[2 c + w]: channels 64 c.., tokens 32 w..
 
       // ---- S^T = Khat Q'^T (log2 units after * sk)
       f32x4 sacc[4];
@@ -1848,8 +1862,8 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
         sacc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const uint32_t d = (uint32_t)__shfl((int)row[ks], 16 * tb + n, 64);
-          const u32x4 av = sm.u.pm1[(d >> (8 * kg)) & 255u];
+          const uint32_t d = row[2 * (ks >> 1) + (tb >> 1)] >> (8 * (2 * (tb & 1) + (ks & 1)));
+          const u32x4 av = sm.u.pm1[d & 255u];
 #pragma unroll
           for (int sp = 0; sp < RP; ++sp) sacc[tb] = mfma16_f16(av, sm.u.qb[ks][sp][lane], sacc[tb]);
         }
