@@ -725,9 +725,24 @@ __device__ __forceinline__ uint64_t merge_list_set(const uint64_t* lists, int fi
       }
       __builtin_amdgcn_s_sleep(1);
     }
+    // one copy of the merge code, rolled over the batch (straight-line copies of it cost
+    // instruction fetches on their first and only run); b[0] is always the next list
+    auto shift = [&]() {
 #pragma unroll
-    for (int i = 0; i < BATCH; ++i)
-      if (c0 + i * step < n_lists) acc = (c0 == first && i == 0) ? b[i] : merge_top64(acc, b[i], lane);
+      for (int r = 0; r + 1 < BATCH; ++r) b[r] = b[r + 1];  // static register moves
+    };
+    int i = 0;
+    if (c0 == first) {  // the first list starts the accumulator
+      acc = b[0];
+      shift();
+      i = 1;
+    }
+    const int nb = (n_lists - c0 + step - 1) / step < BATCH ? (n_lists - c0 + step - 1) / step : BATCH;
+#pragma unroll 1
+    for (; i < nb; ++i) {
+      acc = merge_top64(acc, b[0], lane);
+      shift();
+    }
   }
   return acc;
 }
@@ -1829,7 +1844,7 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   const int32_t* sel = sm.u.sel;
   if (par) {
     uint64_t acc = sm.u.p.part[0][lane];
-#pragma unroll
+#pragma unroll 1
     for (int w = 1; w < 4; ++w) acc = merge_top64(acc, sm.u.p.part[w][63 - lane], lane);
     sm.u.selw[wv_id][lane] = (int32_t)cand_tile(acc);
     wave_lds_sync();
