@@ -44,7 +44,8 @@ enum kvr_dtype { KVR_BF16 = 0, KVR_FP16 = 1, KVR_FP32 = 2 };
 enum kvr_transform { KVR_HADAMARD = 0, KVR_DCT = 1, KVR_NONE = 2 };
 
 /* ABI version of this header (bumped on any signature change; 3 added the ring
- * window, the live state, kvr_cache_append and kvr_set_wait_limit). */
+ * window, the live state, kvr_cache_append and kvr_set_wait_limit; 4 the tile-store
+ * format functions of kvr_store.h). */
 int kvr_abi_version(void);
 
 /* Thread-local description of the last error returned on this thread. */

@@ -14,7 +14,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 constexpr int kMaxTopK = 1024;
 constexpr size_t kAlign = 256;
 

@@ -19,7 +19,7 @@ _DT = {torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32}
 _TORCH_DT = {BF16: torch.bfloat16, FP16: torch.float16, FP32: torch.float32}
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkvr_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -46,6 +46,12 @@ SIGNATURES = {
     "kvr_set_wait_limit": (_I, [_I, _I]),
     "kvr_decode_step_noalloc": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P,
                                      _P, _L, _L, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P]),
+    # tile-store format (include/kvr_store.h): host-only, callable without a GPU
+    "kvr_crc32": (ctypes.c_uint32, [ctypes.c_uint32, _P, _Z]),
+    "kvr_store_payload_bytes": (_L, [_P]),
+    "kvr_store_section": (_L, [_P, _I, _I, _P]),
+    "kvr_store_header_encode": (_I, [_P, _P]),
+    "kvr_store_header_decode": (_I, [_P, _Z, _P]),
 }
 
 _lib = None

@@ -125,6 +125,20 @@ class TileKVCache:
         idx = (torch.arange(self.n, device=self.win_k.device) + self.start) % self.cap
         return self.win_k[:, :, idx], self.win_v[:, :, idx]
 
+    # ------------------------------------------------------------------ files
+    def save(self, f, user=(0, 0, 0, 0)):
+        """Write this layer (tiles, K channel counts, window) as a one-layer store file
+        (include/kvr_store.h; modules/kvr_store.py)."""
+        from . import kvr_store
+        return kvr_store.save(f, [self], user=user)
+
+    @classmethod
+    def load(cls, f, device, reserve_tiles: int = 64, dtype=None) -> "TileKVCache":
+        """The first layer of a store file as a new cache (ring at slot 0)."""
+        from . import kvr_store
+        caches, _ = kvr_store.load(f, device, reserve_tiles=reserve_tiles, dtype=dtype)
+        return caches[0]
+
     # ------------------------------------------------------------------ decode
     def k_tiles(self, top_k_tokens: int) -> int:
         """Tiles selected per KV head: min(max(1, top_k // T), n_tiles) (kvr_retrieval.py:378);

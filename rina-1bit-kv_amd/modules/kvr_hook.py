@@ -179,6 +179,32 @@ class KVRHook:
             return (new_attn,) + tuple(output[1:])
         return hook
 
+    # ------------------------------------------------------------------ files
+    def save_state(self, f):
+        """Every layer's cache plus the decode counters (_context_len, _step) as one store
+        file (include/kvr_store.h): a prompt's state saved once after prefill can be
+        loaded for every request that shares the prompt (prefix caching)."""
+        from . import kvr_store
+        if not self._prefill_done or any(c is None for c in self.caches):
+            raise RuntimeError("nothing to save: run prefill first")
+        return kvr_store.save(f, self.caches, user=(self._context_len, self._step, 0, 0))
+
+    def load_state(self, f):
+        """Replace every layer's cache and the decode counters with a store file written by
+        save_state (same model shape); hooks stay as they are (call register() to decode)."""
+        from . import kvr_store
+        caches, desc = kvr_store.load(f, self.device, reserve_tiles=-(-self.reserve_tokens // self.tile) + 1,
+                                      dtype=self._dtype())
+        if (desc.n_layers, desc.Hkv, desc.W, desc.T, desc.transform) != \
+           (self.n_layers, self.n_kv, self.window_size, self.tile, self.transform):
+            raise ValueError(f"store {desc} does not match this hook (layers={self.n_layers}, n_kv={self.n_kv}, "
+                             f"window={self.window_size}, tile={self.tile}, transform={self.transform})")
+        self.caches = caches
+        self._context_len, self._step = int(desc.user[0]), int(desc.user[1])
+        self._prefill_done = True
+        self._retrieval_built = desc.n_tiles > 0
+        return desc
+
     def check(self):
         """Synchronising status check of every layer (see the module docstring)."""
         for c in self.caches:

@@ -140,6 +140,47 @@ class RetrievalIndex:
         self.tail_v = v_all.float().contiguous()
         self._flush_tiles()
 
+    # ------------------------------------------------------------------ files
+    def save_store(self, f):
+        """Write the store (tiles and the exact staging tail, as the window section with
+        W = 0, fp32) to a store file (include/kvr_store.h).  No reference counterpart: the
+        reference rebuilds its store on reset (kvr_retrieval.py:150-160)."""
+        from . import kvr_store
+        nt, tail = self.n_tiles, self.tail_k.shape[0]
+        desc = kvr_store.new_desc(T=self.tile, transform=self.transform, n_layers=1, B=1, Hkv=self.n_kv,
+                                  n_tiles=nt, W=0, win_len=tail, win_dtype=_hip.FP32, counts=False,
+                                  user=(int(self._calibrated), 0, 0, 0))
+        layer = {kvr_store.SEC_KBITS: self.kbits[:, :nt], kvr_store.SEC_VBITS: self.vbits[:, :nt],
+                 kvr_store.SEC_KSCALE: self.kscale[:, :nt], kvr_store.SEC_VSCALE: self.vscale[:, :nt],
+                 kvr_store.SEC_WIN_K: self.tail_k.permute(1, 0, 2).unsqueeze(0),
+                 kvr_store.SEC_WIN_V: self.tail_v.permute(1, 0, 2).unsqueeze(0)}
+        return kvr_store.write_layers(f, desc, [layer])
+
+    @torch.no_grad()
+    def load_store(self, f):
+        """Replace the store with a store file's first layer (tiles + tail); the file must
+        match this index's KV heads, tile size and transform."""
+        from . import kvr_store
+        desc, layers = kvr_store.read_layers(f)
+        if (desc.B, desc.Hkv, desc.T, desc.transform) != (1, self.n_kv, self.tile, self.transform):
+            raise ValueError(f"store {desc} does not match this index (n_kv={self.n_kv}, tile={self.tile}, "
+                             f"transform={self.transform})")
+        layer, nt = layers[0], int(desc.n_tiles)
+        self._reset_store(cap_tiles=max(16, nt + 1))
+        if nt:
+            for sec, name in ((kvr_store.SEC_KBITS, "kbits"), (kvr_store.SEC_VBITS, "vbits"),
+                              (kvr_store.SEC_KSCALE, "kscale"), (kvr_store.SEC_VSCALE, "vscale")):
+                getattr(self, name)[:, :nt] = torch.from_numpy(layer[sec].copy())
+        self.n_tiles = nt
+        if desc.flags & kvr_store.HAS_WINDOW and desc.win_len:
+            wdt = _hip._TORCH_DT[desc.win_dtype]
+            self.tail_k, self.tail_v = (
+                torch.from_numpy(layer[s].copy()).view(wdt)[0].permute(1, 0, 2).float().contiguous().to(self.device)
+                for s in (kvr_store.SEC_WIN_K, kvr_store.SEC_WIN_V))
+            self._flush_tiles()  # a tail of T or more tokens (W > 0 stores) goes to the tiles
+        self._calibrated = True
+        return desc
+
     def build_attractors(self):
         """k-means attractor basins are not part of the tile codec: no-op."""
         return None

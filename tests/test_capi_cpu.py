@@ -1,7 +1,9 @@
-"""C-ABI checks that need no GPU: the library loads, exports exactly what include/kvr_capi.h
-declares, the ctypes signatures agree with the header, and host-side validation rejects bad
-arguments (every call here fails validation, so nothing is launched)."""
+"""C-ABI checks that need no GPU: the library loads, exports exactly what include/*.h
+(kvr_capi.h, kvr_store.h) declares, the ctypes signatures agree with the headers, and
+host-side validation rejects bad arguments (every call here fails validation, so nothing is
+launched)."""
 import ctypes
+import glob
 import os
 import re
 
@@ -9,7 +11,7 @@ import pytest
 
 from conftest import REPO
 
-HEADER = os.path.join(REPO, "include", "kvr_capi.h")
+HEADERS = sorted(glob.glob(os.path.join(REPO, "include", "*.h")))
 
 
 @pytest.fixture(scope="module")
@@ -24,10 +26,11 @@ def lib(H):
 
 
 def header_functions():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"\b(?:int|size_t|const char\*)\s+(kvr_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.S):
+    for m in re.finditer(r"\b(?:int|int64_t|uint32_t|size_t|const char\*)\s+(kvr_\w+)\s*\(([^;]*?)\)\s*;", text,
+                         flags=re.S):
         args = m.group(2).strip()
         decls[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
     return decls
@@ -35,9 +38,9 @@ def header_functions():
 
 def test_library_exports_every_header_symbol(lib):
     decls = header_functions()
-    assert len(decls) >= 11
+    assert len(HEADERS) == 2 and len(decls) >= 18
     for name in decls:
-        assert hasattr(lib, name), f"{name} declared in kvr_capi.h but not exported"
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
 
 
 def test_ctypes_signatures_match_header(H):
