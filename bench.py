@@ -219,18 +219,21 @@ def kernel_breakdown(wl, steps):
 
 def encode_benchmark(steps, n_seq=32, Hkv=8, N=16384, T=64, tf=H.HADAMARD):
     """Encode K and V (bf16, K with RoPE and outlier channels) of n_seq sequences (or layers)
-    x Hkv heads x N tokens into 1-bit tiles; returns (ms per K+V pair, bytes moved)."""
+    x Hkv heads x N tokens into 1-bit tiles, the K store with its per-tile channel counts (as
+    the product's caches keep it); returns (ms per K+V pair, bytes moved)."""
     K, V = make_kv(n_seq, Hkv, N, 100, "cuda")
     kb, ks = H.alloc_store(n_seq * Hkv, N // T, T, "cuda")
     vb, vs = H.alloc_store(n_seq * Hkv, N // T, T, "cuda")
+    kc = H.alloc_counts(n_seq * Hkv, N // T, "cuda")
 
     def run():
-        H.encode_tiles(K, T, tf, bits=kb, scales=ks)
+        H.encode_tiles(K, T, tf, bits=kb, scales=ks, counts=kc)
         H.encode_tiles(V, T, tf, bits=vb, scales=vs)
 
     ms = time_events(run, steps, 2)
-    nbytes = 2 * n_seq * Hkv * N * D * 2 + 2 * n_seq * Hkv * N * D // 8 + 2 * n_seq * Hkv * (N // T) * 2
-    del K, V, kb, vb
+    nbytes = (2 * n_seq * Hkv * N * D * 2 + 2 * n_seq * Hkv * N * D // 8 + 2 * n_seq * Hkv * (N // T) * 2
+              + n_seq * Hkv * (N // T) * D)
+    del K, V, kb, vb, kc
     torch.cuda.empty_cache()
     return ms, nbytes
 

@@ -12,7 +12,8 @@
 //
 // Two specialisations below take the common cases: T = 64 with a Hadamard (or no)
 // rotation transposes in two 64-channel halves (half the LDS, twice the waves per CU),
-// and a DCT of bf16 input rotates on MFMA.
+// and a DCT of bf16 input rotates on MFMA -- in bulk as a two-stage pipeline of
+// rotating and quantising waves over double-buffered LDS (encode_dct_pipe_kernel).
 //
 // Replaces the int4/int2 packing of RetrievalIndex.batch_append / append
 // (modules/kvr_retrieval.py:162-207) with the 1-bit tile codec.
@@ -297,7 +298,6 @@ __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
                                                  0, 0, 0);
 }
 
-constexpr int DCT_ENC_BLOCKS = 512;  // persistent blocks (two per CU: 66 KB of LDS each at T = 128)
 
 // B operands of wave wv: C^T[in 32 ks + 8 kg + e][out 32 wv + 16 mb + n] in three bf16 parts.
 struct DctOperands {
@@ -429,26 +429,169 @@ __device__ __forceinline__ void encode_tile_dct_mfma(const uint16_t* xs, int64_t
   __syncthreads();  // ys and sbc are rewritten by the next tile
 }
 
-template <int T>
-__global__ __launch_bounds__(256, 2) void encode_dct_mfma_kernel(
+// The bulk DCT encoder (bf16 input): one persistent 384-thread block per CU runs a
+// two-stage pipeline over its tiles.  Step i: waves 0..3 rotate tile i on MFMA (wave w:
+// output channels 32 w .. 32 w + 31, C operands in registers, as encode_tile_dct_mfma)
+// into LDS buffer i % 2 and form the sequential |y| sums of their channels, while waves
+// 4 and 5 quantise tile i - 1 from the other buffer (wave 4 + q: the sigma-delta of
+// channels 64 q + lane); one block barrier ends the step.  The rotating waves keep the
+// next blocks of 16 tokens in flight while they multiply (a tile's last blocks prefetch
+// the next tile's first).  Every operation and its order are those of
+// encode_tile_dct_mfma: the same bits, scales and counts.  Measured per step on MI355X:
+// the rotation's loads (four waves each load the whole tile) dominate (~5 us of MFMA
+// phase against ~1.5 us with the loads taken out), the sigma-delta takes ~2.9 us (128
+// dependent steps per channel).
+constexpr int DCT_PIPE_THREADS = 384;
+
+struct DctPipeTile {
+  int64_t base;  // element offset of the tile's token 0 in x
+  int64_t slot;  // tile slot in the store
+  int64_t dbg;   // element offset of the tile's rotated rows in dbg
+};
+
+__device__ __forceinline__ DctPipeTile dct_pipe_tile(int64_t blk, int T, int64_t n_h, int64_t n_tiles, int64_t n_tok,
+                                                     int64_t sb, int64_t sh, int64_t st, int64_t ots, int64_t oto) {
+  const int64_t seg = blk / n_tiles;
+  const int64_t tile = blk - seg * n_tiles;
+  const int64_t b = seg / n_h;
+  const int64_t h = seg - b * n_h;
+  return DctPipeTile{b * sb + h * sh + tile * T * st, seg * ots + oto + tile, (seg * n_tok + tile * T) * D};
+}
+
+// A operands of 16 tokens of a tile: token 16 j + n, inputs 32 ks + 8 kg .. + 7.
+__device__ __forceinline__ void dct_pipe_load(const uint16_t* xs, int64_t stride_t, int lane, u32x4 (&xa)[4]) {
+  const uint16_t* xr = xs + (int64_t)(lane & 15) * stride_t + 8 * (lane >> 4);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) xa[ks] = *(const u32x4*)(xr + 32 * ks);
+}
+
+template <int T, bool DBG>
+__global__ __launch_bounds__(DCT_PIPE_THREADS, 1) void encode_dct_pipe_kernel(
     const uint16_t* __restrict__ x, int64_t n_h, int64_t n_tiles, int64_t n_tok, int64_t stride_b,
     int64_t stride_h, int64_t stride_t, uint64_t* __restrict__ bits, uint16_t* __restrict__ scales,
     int64_t out_tile_stride, int64_t out_tile_offset, float* __restrict__ dbg,
     uint8_t* __restrict__ counts, int64_t n_blk) {
+  constexpr int LDW = T + 1;      // padded row
   constexpr int W = T / 64;
-  __shared__ float ys[D * (T + 1)];
-  __shared__ DctTileSmem sm;
-  DctOperands o;
-  dct_operands(o, threadIdx.x >> 6, threadIdx.x & 63);
-  for (int64_t blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
-    const int64_t seg = blk / n_tiles;
-    const int64_t tile = blk - seg * n_tiles;
-    const int64_t b = seg / n_h;
-    const int64_t h = seg - b * n_h;
-    const int64_t slot = seg * out_tile_stride + out_tile_offset + tile;
-    encode_tile_dct_mfma<T>(x + b * stride_b + h * stride_h + tile * T * stride_t, stride_t, o,
-                            bits + slot * (int64_t)(D * W), scales + slot, counts ? counts + slot * D : nullptr,
-                            dbg ? dbg + (seg * n_tok + tile * T) * D : nullptr, ys, sm);
+  constexpr int NBATCH = T / 64;  // 64-token load batches per tile
+  __shared__ float ys[2][D * LDW];
+  __shared__ float ssum[2][D];  // per-channel sums of |y| (tile i in buffer i % 2)
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t G = gridDim.x;
+  const int64_t n_my = (blockIdx.x < n_blk) ? (n_blk - 1 - blockIdx.x) / G + 1 : 0;  // this block's tiles
+  auto tile_of = [&](int64_t i) {
+    return dct_pipe_tile(blockIdx.x + i * G, T, n_h, n_tiles, n_tok, stride_b, stride_h, stride_t,
+                         out_tile_stride, out_tile_offset);
+  };
+
+  if (wv < 4) {  // ---------------- rotating waves
+    const int n = lane & 15;
+    const int kg = lane >> 4;
+    DctOperands o;
+    dct_operands(o, wv, lane);
+    // A operands of 4 blocks of 16 tokens: block j holds tokens 64 bi + 16 j + .. of batch bi;
+    // once a block's products are issued its registers load the same block of the next
+    // batch (this tile's next 64 tokens, or the next tile's first), so three blocks of
+    // loads are in flight behind every block of products
+    u32x4 xa[4][4];
+    if (n_my > 0) {
+      const int64_t b0 = tile_of(0).base;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dct_pipe_load(x + b0 + (int64_t)16 * j * stride_t, stride_t, lane, xa[j]);
+    }
+    for (int64_t i = 0; i < n_my; ++i) {
+      const DctPipeTile tl = tile_of(i);
+      const bool has_next = i + 1 < n_my;
+      const int64_t next_base = has_next ? tile_of(i + 1).base : 0;
+      float* Y = ys[i & 1];
+#pragma unroll
+      for (int bi = 0; bi < NBATCH; ++bi) {
+        const bool more = bi + 1 < NBATCH || has_next;  // a next batch to load
+        const int64_t nb = (bi + 1 < NBATCH) ? tl.base + (int64_t)64 * (bi + 1) * stride_t : next_base;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // the two output blocks' accumulation chains interleaved (each product's
+          // predecessor in its chain is two instructions back); per chain the order of
+          // encode_tile_dct_mfma
+          f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+              for (int mb = 0; mb < 2; ++mb) acc[mb] = mfma_bf16(xa[j][ks], o.cb[mb][ks][p], acc[mb]);
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb) {
+            // acc[mb][r] = Y[token 64 bi + 16 j + 4 kg + r][out 32 wv + 16 mb + n]
+            const int ch = 32 * wv + 16 * mb + n;
+            const int t0 = 64 * bi + 16 * j + 4 * kg;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Y[ch * LDW + t0 + r] = acc[mb][r];
+            if constexpr (DBG) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) dbg[tl.dbg + (int64_t)(t0 + r) * D + ch] = acc[mb][r];
+            }
+          }
+          if (more) dct_pipe_load(x + nb + (int64_t)16 * j * stride_t, stride_t, lane, xa[j]);
+          __builtin_amdgcn_sched_barrier(0);  // keeps each block's loads behind its products (one register set)
+        }
+      }
+      if (lane < 32) {  // the sequential |y| sum of each of the wave's 32 channels (its own LDS writes)
+        const float* yc = Y + (32 * wv + lane) * LDW;
+        float sa = 0.f;
+#pragma unroll 32
+        for (int t = 0; t < T; ++t) sa = sa + fabsf(yc[t]);
+        ssum[i & 1][32 * wv + lane] = sa;
+      }
+      __syncthreads();
+    }
+    __syncthreads();  // the quantisers' last step
+  } else {  // ---------------- quantising waves (q = 0, 1)
+    const int q = wv - 4;
+    for (int64_t i = 0; i <= n_my; ++i) {
+      if (i >= 1) {
+        const DctPipeTile tl = tile_of(i - 1);
+        const float* Y = ys[(i - 1) & 1];
+        const float* y0 = Y + lane * LDW;
+        const float* y1 = Y + (lane + 64) * LDW;
+        float a = ssum[(i - 1) & 1][lane] + ssum[(i - 1) & 1][lane + 64];  // tree step j += j + 64, then the lane tree
+        a = a + xor_lane_f<32>(a);
+        a = a + xor_lane_f<16>(a);
+        a = a + xor_lane_f<8>(a);
+        a = a + xor_lane_f<4>(a);
+        a = a + xor_lane_f<2>(a);
+        a = a + xor_lane_f<1>(a);
+        float mean = a * (1.0f / (float)(T * D));
+        mean = (mean < FP16_MAX) ? mean : FP16_MAX;
+        const uint32_t s16 = f32_to_f16_rne(mean);
+        const float s32 = f16_to_f32(s16);
+        const int c = 64 * q + lane;
+        const float* yr = q ? y1 : y0;
+        uint64_t* out = bits + tl.slot * (int64_t)(D * W) + c * W;
+        float e = 0.f;
+        int pc = 0;
+#pragma unroll 1
+        for (int w = 0; w < W; ++w) {  // one 64-token word at a time (bounded register use)
+          uint32_t h[2] = {0u, 0u};
+#pragma unroll
+          for (int t = 0; t < 64; ++t) {
+            const float u = yr[64 * w + t] + e;
+            h[t >> 5] |= (uint32_t)(u >= 0.f) << (t & 31);
+            // (u >= 0 ? s : -s) as copysign(s, u): u is never -0 (e never is: it starts at +0
+            // and x - x rounds to +0), and a NaN u gives a NaN e either way -- the same bits,
+            // with the bit test off the e chain
+            e = u - __builtin_copysignf(s32, u);
+          }
+          out[w] = ((uint64_t)h[1] << 32) | h[0];
+          pc += __builtin_popcount(h[0]) + __builtin_popcount(h[1]);
+        }
+        if (q == 0 && lane == 0) scales[tl.slot] = (uint16_t)s16;
+        if (counts) counts[tl.slot * D + c] = (uint8_t)pc;  // set bits over the tile's T tokens (<= 128)
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -462,13 +605,19 @@ static hipError_t launch_encode_t(int T, const void* x, int64_t n_b, int64_t n_h
   if (nblk == 0) return hipSuccess;
   dim3 grid((unsigned)nblk), block(64);
   if (DT == KVR_BF16 && TF == KVR_DCT) {
-    const dim3 pgrid((unsigned)(nblk < DCT_ENC_BLOCKS ? nblk : DCT_ENC_BLOCKS));
-    if (T == 64)
-      hipLaunchKernelGGL(encode_dct_mfma_kernel<64>, pgrid, dim3(256), 0, s, (const uint16_t*)x, n_h, n_tiles,
-                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts, nblk);
-    else
-      hipLaunchKernelGGL(encode_dct_mfma_kernel<128>, pgrid, dim3(256), 0, s, (const uint16_t*)x, n_h, n_tiles,
-                         n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts, nblk);
+    int dev = 0, n_cu = 0;  // one persistent block per CU (the pipeline's LDS fills the CU)
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+      n_cu = 256;
+    const dim3 pgrid((unsigned)(nblk < n_cu ? nblk : n_cu));
+#define KVR_DCT_PIPE(TV, DBGV)                                                                               \
+  hipLaunchKernelGGL((encode_dct_pipe_kernel<TV, DBGV>), pgrid, dim3(DCT_PIPE_THREADS), 0, s, (const uint16_t*)x, \
+                     n_h, n_tiles, n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts, nblk)
+    if (T == 64 && dbg) KVR_DCT_PIPE(64, true);
+    else if (T == 64) KVR_DCT_PIPE(64, false);
+    else if (dbg) KVR_DCT_PIPE(128, true);
+    else KVR_DCT_PIPE(128, false);
+#undef KVR_DCT_PIPE
   } else if (T == 64 && TF != KVR_DCT)
     hipLaunchKernelGGL((encode_tiles64_kernel<DT, TF == KVR_DCT ? KVR_NONE : TF>), grid, block, 0, s, x,
                        n_h, n_tiles, n_tok, sb, sh, st, bits, scales, ots, oto, dbg, counts);
