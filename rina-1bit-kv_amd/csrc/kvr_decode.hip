@@ -1776,9 +1776,11 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   // Selection (when asked).  From more than 8 candidate lists: every wave first rotates
   // its query heads (the lists are usually still being written), then merges lists
   // w, w + 4, ... into a partial top 64; the four partials meet in LDS and every wave
-  // merges them (the same result in each) into its own copy of the selection.  From
-  // fewer lists (one load batch) or the scores: wave 0 selects while waves 1..3 rotate
-  // the query heads.  A selection whose bounded wait gave up poisons the item's record.
+  // merges them (the same result in each) into its own copy of the selection.  (Merging
+  // first, polling from the item's start, and rotating while the first tile's words are
+  // in flight measured 3.6 us slower at configs[4].)  From fewer lists (one load batch)
+  // or the scores: wave 0 selects while waves 1..3 rotate the query heads.  A selection
+  // whose bounded wait gave up poisons the item's record.
   const bool par = do_sel && a.cand && a.n_chunks > 8;  // more than one load batch
   const int qw0 = (do_sel && !par) ? 1 : 0;
   uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
@@ -1786,17 +1788,15 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
                            : CAND_EPOCH_CHAIN;  // the lists' tag epoch
   if (a.wait_fail && epoch_word) ep ^= WAIT_FAIL_EPOCH;  // test hook: no list carries this tag
   bool failed = false;
-  if (do_sel && !par && wv_id == 0) {
-    failed = select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane, ep);
-    wave_lds_sync();
-    if (rs == 0)
-      for (int i = lane; i < kp; i += 64) a.idx[seg * kp + i] = (i < k) ? sm.u.sel[i] : -1;
-  }
-  if (wv_id >= qw0) {
-    uint32_t r0[QH_MAX], r1[QH_MAX];
+  const bool rot_wave = wv_id >= qw0;
+  uint32_t r0[QH_MAX], r1[QH_MAX];  // the wave's query heads, loaded first
+  DctRegs dt{};
+  if (rot_wave) {
     load_heads_raw<QT>(a, b, h, wv_id - qw0, 4 - qw0, lane, r0, r1);
-    DctRegs dt{};
     if (a.transform == KVR_DCT) dt = dct_table_load(lane);  // in flight with the query loads
+  }
+  // Q'^T operands: the wave's heads rotated into the B-operand layout
+  auto rotate_heads = [&]() {
     float v0[QH_MAX], v1[QH_MAX];
     load_heads_cvt<QT>(a, r0, r1, v0, v1);
     if (a.transform == KVR_DCT) dct_table_store(dt, sm.u.xs[wv_id], lane);
@@ -1822,7 +1822,14 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
         for (int sp = 0; sp < RP; ++sp) q32[sp * 64 * 4 + (lane & 3)] = pack2(p0[sp], p1[sp]);
       }
     }
+  };
+  if (do_sel && !par && wv_id == 0) {
+    failed = select_tiles(a, seg, k, sm.u.sel, sm.u.p.tk, lane, ep);
+    wave_lds_sync();
+    if (rs == 0)
+      for (int i = lane; i < kp; i += 64) a.idx[seg * kp + i] = (i < k) ? sm.u.sel[i] : -1;
   }
+  if (rot_wave) rotate_heads();
   if (par)
     sm.u.p.part[wv_id][lane] = merge_list_set(a.cand + seg * a.n_chunks_cap * (int64_t)128, wv_id, 4, a.n_chunks,
                                               lane, ep, seg, a.ctr ? a.ctr + CTR_ERR_WORD : nullptr, a.spin_max,
