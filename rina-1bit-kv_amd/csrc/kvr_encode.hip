@@ -432,15 +432,16 @@ __device__ __forceinline__ void encode_tile_dct_mfma(const uint16_t* xs, int64_t
 // The bulk DCT encoder (bf16 input): one persistent 384-thread block per CU runs a
 // two-stage pipeline over its tiles.  Step i: waves 0..3 rotate tile i on MFMA (wave w:
 // output channels 32 w .. 32 w + 31, C operands in registers, as encode_tile_dct_mfma)
-// into LDS buffer i % 2 and form the sequential |y| sums of their channels, while waves
-// 4 and 5 quantise tile i - 1 from the other buffer (wave 4 + q: the sigma-delta of
-// channels 64 q + lane); one block barrier ends the step.  The rotating waves keep the
+// into LDS buffer i % 2, while waves 4 and 5 quantise tile i - 1 from the other buffer
+// (each forms all 128 channel |y| sums -- lane: channels lane and lane + 64, two chains --
+// so both hold the tile scale without an exchange; then wave 4 + q runs the sigma-delta
+// of channels 64 q + lane); one block barrier ends the step.  The rotating waves keep the
 // next blocks of 16 tokens in flight while they multiply (a tile's last blocks prefetch
 // the next tile's first).  Every operation and its order are those of
 // encode_tile_dct_mfma: the same bits, scales and counts.  Measured per step on MI355X:
 // the rotation's loads (four waves each load the whole tile) dominate (~5 us of MFMA
-// phase against ~1.5 us with the loads taken out), the sigma-delta takes ~2.9 us (128
-// dependent steps per channel).
+// phase against ~1.5 us with the loads taken out); the quantisers need ~4 us (the sums,
+// then 128 dependent sigma-delta steps per channel).
 constexpr int DCT_PIPE_THREADS = 384;
 
 struct DctPipeTile {
@@ -475,7 +476,6 @@ __global__ __launch_bounds__(DCT_PIPE_THREADS, 1) void encode_dct_pipe_kernel(
   constexpr int W = T / 64;
   constexpr int NBATCH = T / 64;  // 64-token load batches per tile
   __shared__ float ys[2][D * LDW];
-  __shared__ float ssum[2][D];  // per-channel sums of |y| (tile i in buffer i % 2)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -538,13 +538,6 @@ __global__ __launch_bounds__(DCT_PIPE_THREADS, 1) void encode_dct_pipe_kernel(
           __builtin_amdgcn_sched_barrier(0);  // keeps each block's loads behind its products (one register set)
         }
       }
-      if (lane < 32) {  // the sequential |y| sum of each of the wave's 32 channels (its own LDS writes)
-        const float* yc = Y + (32 * wv + lane) * LDW;
-        float sa = 0.f;
-#pragma unroll 32
-        for (int t = 0; t < T; ++t) sa = sa + fabsf(yc[t]);
-        ssum[i & 1][32 * wv + lane] = sa;
-      }
       __syncthreads();
     }
     __syncthreads();  // the quantisers' last step
@@ -556,7 +549,13 @@ __global__ __launch_bounds__(DCT_PIPE_THREADS, 1) void encode_dct_pipe_kernel(
         const float* Y = ys[(i - 1) & 1];
         const float* y0 = Y + lane * LDW;
         const float* y1 = Y + (lane + 64) * LDW;
-        float a = ssum[(i - 1) & 1][lane] + ssum[(i - 1) & 1][lane + 64];  // tree step j += j + 64, then the lane tree
+        float s0 = 0.f, s1 = 0.f;  // the sequential |y| sums of channels lane and lane + 64
+#pragma unroll 16
+        for (int t = 0; t < T; ++t) {
+          s0 = s0 + fabsf(y0[t]);
+          s1 = s1 + fabsf(y1[t]);
+        }
+        float a = s0 + s1;  // tree step j += j + 64, then the lane tree
         a = a + xor_lane_f<32>(a);
         a = a + xor_lane_f<16>(a);
         a = a + xor_lane_f<8>(a);
