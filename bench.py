@@ -20,6 +20,7 @@ Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-enco
        python bench.py --copy-calibration   (plain copy kernel for rocprof counter scaling)
 """
 import argparse
+import subprocess
 import json
 import math
 import os
@@ -355,13 +356,24 @@ def _timed(fn, reps=5):
 
 
 def _cpu_model():
+    """The host CPU as lscpu names it (else /proc/cpuinfo), with its AVX-512 capability."""
+    name, avx512 = "unknown", False
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if line.startswith("model name") and name == "unknown":
+                name = line.split(":", 1)[1].strip()
+            if line.startswith("flags"):
+                avx512 = "avx512f" in line.split()
     except OSError:
         pass
-    return "unknown"
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                name = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return f"{name} ({'AVX-512' if avx512 else 'no AVX-512'})"
 
 
 def cpu_threads():

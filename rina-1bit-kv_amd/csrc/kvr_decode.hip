@@ -2468,8 +2468,13 @@ __global__ __launch_bounds__(NT) void select_score_kernel(DecodeArgs a) {
 // Launch 2: per segment its n_rparts retrieved items (one selected tile per wave)
 // followed by its n_wparts window items; the latency-bound retrieved items run
 // between the streaming window items.
+// The VALU retrieval method's LDS (RetSmem<G4>) allows 2 blocks per CU at G4 = 8 and 1 at
+// G4 = 16; the launch bound asks for what fits.
+constexpr int attend_min_blocks(int RM, int G4) {
+  return RM == 1 ? (G4 >= 16 ? 1 : (G4 >= 8 ? 2 : KVR_ATTEND_WAVES)) : KVR_ATTEND_WAVES;
+}
 template <int T, int WDT, int QS, int RM, int G4>
-__global__ __launch_bounds__(NT, KVR_ATTEND_WAVES) void attend_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(NT, attend_min_blocks(RM, G4)) void attend_kernel(DecodeArgs a) {
   __shared__ union {
     WindowSmem win;
     RetSmem<G4> ret;
