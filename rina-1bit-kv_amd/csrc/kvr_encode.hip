@@ -486,6 +486,9 @@ __global__ __launch_bounds__(DCT_PIPE_THREADS, 1) void encode_dct_pipe_kernel(
                          out_tile_stride, out_tile_offset);
   };
 
+  // The two roles run separate loops (each keeps only its own state in registers); both
+  // execute n_my + 1 block barriers, one per step, so every s_barrier of the block is met by
+  // all six waves (the hardware barrier counts waves, not code locations).
   if (wv < 4) {  // ---------------- rotating waves
     const int n = lane & 15;
     const int kg = lane >> 4;
@@ -579,8 +582,8 @@ __global__ __launch_bounds__(DCT_PIPE_THREADS, 1) void encode_dct_pipe_kernel(
             const float u = yr[64 * w + t] + e;
             h[t >> 5] |= (uint32_t)(u >= 0.f) << (t & 31);
             // (u >= 0 ? s : -s) as copysign(s, u): u is never -0 (e never is: it starts at +0
-            // and x - x rounds to +0), and a NaN u gives a NaN e either way -- the same bits,
-            // with the bit test off the e chain
+            // and x - x rounds to +0), and for a NaN u both give e = u - (+-s), the NaN of u --
+            // the same bits, with the bit test off the e chain
             e = u - __builtin_copysignf(s32, u);
           }
           out[w] = ((uint64_t)h[1] << 32) | h[0];
