@@ -1778,9 +1778,9 @@ __device__ void retrieved_role_mfma(const DecodeArgs& a, int64_t seg, int rs, Re
   // w, w + 4, ... into a partial top 64; the four partials meet in LDS and every wave
   // merges them (the same result in each) into its own copy of the selection.  (Merging
   // first, polling from the item's start, and rotating while the first tile's words are
-  // in flight measured 3.6 us slower at configs[4].)  From fewer lists (one load batch)
-  // or the scores: wave 0 selects while waves 1..3 rotate the query heads.  A selection
-  // whose bounded wait gave up poisons the item's record.
+  // in flight measured 3.6 us slower with 16 lists at T = 128.)  From fewer lists (one
+  // load batch) or the scores: wave 0 selects while waves 1..3 rotate the query heads.  A
+  // selection whose bounded wait gave up poisons the item's record.
   const bool par = do_sel && a.cand && a.n_chunks > 8;  // more than one load batch
   const int qw0 = (do_sel && !par) ? 1 : 0;
   uint32_t ep = epoch_word ? (uint32_t)__hip_atomic_load(epoch_word, __ATOMIC_RELAXED,
@@ -2020,8 +2020,9 @@ __device__ __forceinline__ void merge_sums(const DecodeArgs& a, int64_t seg, int
   const int64_t rs = a.g * (2 + D);
   const float* R0 = rec_ptr(a, seg, 0);
   // batches of 8, 20 or 32 parts: few more loads than parts (the merge code runs once,
-  // fetched from L2, so every unused unrolled load costs time: 20 parts, the configs[4]
-  // segment, measured ~1 us faster than a batch of 32)
+  // fetched from L2, so every unused unrolled load costs time: a segment of 20 parts -- 16
+  // retrieved items of 4 tiles of 128 and 4 window items -- merged ~1 us faster than with a
+  // batch of 32)
   float M = -__builtin_inff();
   L = w0 = w1 = r0 = r1 = 0.f;
   if (n_parts <= 8) merge_parts<8>(a, R0, rs, i, lane, M, L, w0, w1, r0, r1);
